@@ -1,0 +1,66 @@
+"""Build recipe for the gfx950 shared library ``libfields_amd.so``.
+
+The library is compiled in-tree with ``hipcc --offload-arch=gfx950`` and loaded with ctypes
+(:mod:`fields_lm_amd._native`). It links against the HIP runtime by SONAME
+(``libamdhip64.so.7``), so when PyTorch-ROCm is imported first the process keeps a single HIP
+runtime: PyTorch's.
+
+Run ``python -m fields_lm_amd.build`` or call :func:`build`.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+REPO_DIR = PKG_DIR.parent
+SOURCES = [PKG_DIR / "csrc" / "field_scan.hip"]
+INCLUDE_DIR = REPO_DIR / "include"
+LIB_PATH = PKG_DIR / "libfields_amd.so"
+ARCH = "gfx950"
+
+# -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code (the compiler would
+# otherwise form them from float2-shaped arithmetic).
+HIP_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-ffp-contract=fast",
+    "-Wall",
+    "-Wno-unused-function",
+]
+
+
+def hipcc() -> str:
+    found = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not Path(found).exists():
+        raise RuntimeError("hipcc not found; the ROCm toolchain is required to build libfields_amd.so")
+    return found
+
+
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None) -> Path:
+    """Compile the HIP sources into ``libfields_amd.so`` (always recompiles)."""
+    target = Path(out) if out is not None else LIB_PATH
+    tmp = target.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIP_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}",
+           *[str(s) for s in SOURCES], "-o", str(tmp)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    env = dict(os.environ)
+    proc = subprocess.run(cmd, capture_output=True, text=True, env=env)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
+    if verbose and proc.stderr.strip():
+        print(proc.stderr, file=sys.stderr)
+    os.replace(tmp, target)
+    return target
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

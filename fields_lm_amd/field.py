@@ -1,0 +1,327 @@
+"""Field recurrence ops and the drop-in Field mixer / block modules (HIP path only).
+
+Reference: src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py ("canon").
+
+* :func:`fused_field_read`      — same call as canon:1108-1123; runs ``fl_scan_forward``.
+* :func:`field_decode_step`     — single-token step (no reference counterpart), ``fl_decode_step``.
+* :class:`IndependentVacancyField`, :class:`FieldBlock`, :class:`RMSNorm`,
+  :class:`PackedSwiGLU` — same constructor signatures, parameter names, initialisation order
+  and forward maths as canon:1131-1221 and canon:300-325, so a reference state_dict loads
+  with ``strict=True`` and a seeded construction yields identical parameters.
+
+The scan runs only on a ROCm device through ``libfields_amd.so``. There is no CPU path and no
+fallback: a CPU tensor or a missing library raises, as the reference's Triton path does
+(canon:923-926).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import _native as nat
+
+VAC_MAX = 0.90  # canon:68
+BACKENDS = ("reference", "triton", "hip")
+
+
+# ======================================================================================
+# scan ops
+# ======================================================================================
+
+def _check_scan_inputs(raw: torch.Tensor, tr: torch.Tensor):
+    """Argument checks of canon:923-938, in the same order and with the same exception types."""
+    if not raw.is_cuda:
+        raise RuntimeError("Chunked Field kernel requires a ROCm (cuda) device")
+    if raw.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"raw must be float32 or bfloat16, got {raw.dtype}")
+    if raw.ndim != 3:
+        raise ValueError(raw.shape)
+    batch, length, three_channels = raw.shape
+    if three_channels % 3:
+        raise ValueError(raw.shape)
+    channels = three_channels // 3
+    if tr.numel() != channels:
+        raise ValueError((raw.shape, tr.shape))
+    return batch, length, channels
+
+
+def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+               gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
+               return_state: bool = False, algo: int = nat.FL_ALGO_AUTO):
+    """Run the HIP scan. Returns ``read`` fp32 [B,T,4C] (and the final planar state [B,2C]).
+
+    raw: fp32 or bf16 [B,T,3C] on a ROCm device, channel stride 1 (other strides are passed
+    through). state_in: fp32 [B,2C] planar (re | im) or None for the zero state.
+    """
+    lib = nat.load()
+    batch, length, channels = _check_scan_inputs(raw, transition_r)
+    if raw.stride(2) != 1:
+        raw = raw.contiguous()
+    dev = raw.device
+    tr = transition_r.detach().to(device=dev, dtype=torch.float32).contiguous()
+    ti = transition_i.detach().to(device=dev, dtype=torch.float32).contiguous()
+    gm = gamma.detach().to(device=dev, dtype=torch.float32).contiguous()
+    if ti.numel() != channels or gm.numel() != channels:
+        raise ValueError((raw.shape, transition_i.shape, gamma.shape))
+    read = torch.empty((batch, length, 4 * channels), device=dev, dtype=torch.float32)
+    sin = None
+    if state_in is not None:
+        if state_in.shape != (batch, 2 * channels):
+            raise ValueError(f"state_in must be [B, 2C] = {(batch, 2 * channels)}, got {tuple(state_in.shape)}")
+        sin = state_in.detach().to(device=dev, dtype=torch.float32).contiguous()
+    sout = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32) if return_state else None
+    if batch == 0 or length == 0 or channels == 0:
+        if sout is not None:
+            sout.copy_(sin if sin is not None else torch.zeros_like(sout))
+        return (read, sout) if return_state else read
+    ws_bytes = int(lib.fl_scan_workspace_bytes(batch, length, channels))
+    workspace = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    code = lib.fl_scan_forward_ex(
+        nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels,
+        raw.stride(0), raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
+        nat.ptr(sout), nat.ptr(read), nat.FL_DTYPE_F32, nat.ptr(workspace), ws_bytes, algo,
+        nat.stream_handle(dev))
+    nat.check(code, "fl_scan_forward")
+    return (read, sout) if return_state else read
+
+
+class _FieldReadFunction(torch.autograd.Function):
+    """Forward of canon:912-1018 on the HIP path. The backward kernels are not built yet."""
+
+    @staticmethod
+    def forward(ctx, raw, transition_r, transition_i, gamma, block_c, chunk_t):
+        return field_scan(raw, transition_r, transition_i, gamma)
+
+    @staticmethod
+    def backward(ctx, grad_read):
+        raise NotImplementedError(
+            "the HIP Field scan is forward-only: its backward (canon:1020-1105) is not implemented")
+
+
+def fused_field_read(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+                     gamma: torch.Tensor, block_c: int = 32, chunk_t: int = 64) -> torch.Tensor:
+    """Drop-in for canon:1108-1123 ``fused_field_read``.
+
+    ``block_c`` / ``chunk_t`` are the Triton kernels' tile sizes; they do not change the result
+    and are accepted for call compatibility. The HIP kernels choose their own tiling.
+    Unlike the reference, bf16 ``raw`` is accepted as well (upcast in-register, exactly).
+    """
+    return _FieldReadFunction.apply(raw, transition_r, transition_i, gamma, block_c, chunk_t)
+
+
+def field_decode_step(raw_t: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+                      gamma: torch.Tensor, state: torch.Tensor,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One recurrent step: ``state`` (fp32 [B,2C] planar) is updated in place; returns read_t
+    fp32 [B,4C]. Equal to row t of :func:`field_scan` when ``state`` holds s[t-1].
+
+    Static shapes, no host synchronisation: capturable in a HIP graph.
+    """
+    lib = nat.load()
+    if not raw_t.is_cuda:
+        raise RuntimeError("Field decode step requires a ROCm (cuda) device")
+    if raw_t.ndim != 2 or raw_t.shape[1] % 3:
+        raise ValueError(raw_t.shape)
+    batch, channels = raw_t.shape[0], raw_t.shape[1] // 3
+    if transition_r.numel() != channels:
+        raise ValueError((raw_t.shape, transition_r.shape))
+    if raw_t.stride(1) != 1:
+        raw_t = raw_t.contiguous()
+    if state.shape != (batch, 2 * channels) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError("state must be a contiguous fp32 [B, 2C] tensor")
+    for p in (transition_r, transition_i, gamma):
+        if p.dtype != torch.float32 or not p.is_contiguous() or p.device != raw_t.device:
+            raise ValueError("transition_r/transition_i/gamma must be contiguous fp32 on the raw device")
+    if out is None:
+        out = torch.empty((batch, 4 * channels), device=raw_t.device, dtype=torch.float32)
+    code = lib.fl_decode_step(nat.ptr(raw_t), nat.dtype_code(raw_t.dtype), batch, channels,
+                              raw_t.stride(0), nat.ptr(transition_r), nat.ptr(transition_i),
+                              nat.ptr(gamma), nat.ptr(state), nat.ptr(out), nat.FL_DTYPE_F32,
+                              nat.stream_handle(raw_t.device))
+    nat.check(code, "fl_decode_step")
+    return out
+
+
+def state_to_complex(state: torch.Tensor) -> torch.Tensor:
+    """Planar [B,2C] fp32 state -> complex64 [B,C]."""
+    c = state.shape[-1] // 2
+    return torch.complex(state[..., :c], state[..., c:])
+
+
+# ======================================================================================
+# modules (canon:300-325, 1131-1221)
+# ======================================================================================
+
+class RMSNorm(nn.Module):
+    """canon:300-309: fp32 normalisation, result cast back to the input dtype."""
+
+    def __init__(self, dim: int, eps: float = 1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        y = xf * torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class PackedSwiGLU(nn.Module):
+    """canon:312-325: w12 packs (gate, value); out = w3(silu(gate) * value)."""
+
+    def __init__(self, dim: int, hidden: Optional[int] = None):
+        super().__init__()
+        self.hidden = int(hidden) if hidden is not None else ((int(8 * dim / 3) + 63) // 64) * 64
+        self.w12 = nn.Linear(dim, 2 * self.hidden, bias=False)
+        self.w3 = nn.Linear(self.hidden, dim, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, value = self.w12(x).chunk(2, dim=-1)
+        return self.w3(F.silu(gate) * value)
+
+
+class IndependentVacancyField(nn.Module):
+    """Zero-attention Field mixer with independent vacancy and displaced readout (canon:1131-1195).
+
+    Every backend name of the reference is accepted ("reference", "triton"; plus "hip"); all
+    of them run the HIP scan, the one implementation this package has.
+    """
+
+    def __init__(self, dim: int, backend: str, field_chunk: int, triton_block_c: int,
+                 triton_chunk_t: int):
+        super().__init__()
+        if dim % 2:
+            raise ValueError("Field dim must be even")
+        if backend not in BACKENDS:
+            raise ValueError(backend)
+        self.dim = dim
+        self.channels = dim // 2
+        self.backend = backend
+        self.field_chunk = int(field_chunk)
+        self.triton_block_c = int(triton_block_c)
+        self.triton_chunk_t = int(triton_chunk_t)
+        # parameter creation order fixes the RNG stream: write_proj, out_proj, gate_proj
+        self.write_proj = nn.Linear(dim, dim + self.channels)
+        ring = torch.linspace(0.85, 0.999, self.channels)
+        self.radius_logit = nn.Parameter(torch.log(ring / (1.0 - ring)))
+        self.theta = nn.Parameter(torch.linspace(0.03, math.pi * 0.97, self.channels))
+        self.read_norm = RMSNorm(2 * dim)
+        self.out_proj = nn.Linear(2 * dim, dim)
+        self.gate_proj = nn.Linear(dim, dim)
+
+    def transition(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """(tr, ti, gamma) fp32 [C] (canon:1169-1173), computed in the parameters' dtype."""
+        radius = torch.sigmoid(self.radius_logit).clamp(0.50, 0.99995).float()
+        theta = self.theta.float()
+        tr = radius * torch.cos(theta)
+        ti = radius * torch.sin(theta)
+        gamma = torch.sqrt((1.0 - radius.square()).clamp_min(1e-4))
+        return tr.contiguous(), ti.contiguous(), gamma.contiguous()
+
+    def _raw(self, x: torch.Tensor) -> torch.Tensor:
+        # bf16 (autocast) and fp32 raw go to the kernel as they are; the kernel's upcast of
+        # bf16 is exact, so this equals the reference's `.contiguous().float()` copy.
+        raw = self.write_proj(x)
+        if raw.dtype not in (torch.float32, torch.bfloat16):
+            raw = raw.float()
+        return raw
+
+    def _readout(self, x: torch.Tensor, read: torch.Tensor) -> torch.Tensor:
+        out = self.out_proj(self.read_norm(read))
+        gate = torch.sigmoid(self.gate_proj(x))
+        return x + (out * gate).to(x.dtype)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        tr, ti, gamma = self.transition()
+        read = fused_field_read(self._raw(x), tr, ti, gamma, self.triton_block_c, self.triton_chunk_t)
+        return self._readout(x, read)
+
+    def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """Forward over [B,T,dim] that also returns the recurrent state s[T-1] (fp32 [B,2C]).
+
+        ``state`` continues a previous segment (state_in); None starts from zero as forward does.
+        """
+        tr, ti, gamma = self.transition()
+        read, new_state = field_scan(self._raw(x), tr, ti, gamma, state_in=state, return_state=True)
+        return self._readout(x, read), new_state
+
+    def step(self, x_t: torch.Tensor, state: torch.Tensor,
+             params: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+        """One decode token: x_t [B,dim] -> [B,dim]; ``state`` [B,2C] fp32 is advanced in place.
+
+        ``params`` = a cached ``self.transition()`` (recomputed when None).
+        """
+        tr, ti, gamma = params if params is not None else self.transition()
+        read_t = field_decode_step(self._raw(x_t), tr, ti, gamma, state)
+        return self._readout(x_t, read_t)
+
+    def new_state(self, batch: int, device=None) -> torch.Tensor:
+        return torch.zeros((batch, 2 * self.channels), device=device, dtype=torch.float32)
+
+
+class FieldBlock(nn.Module):
+    """canon:1198-1221: x = mixer(x) (residual inside); x + ff(ff_norm(x))."""
+
+    def __init__(self, dim: int, backend: str, field_chunk: int, triton_block_c: int,
+                 triton_chunk_t: int, ff_hidden: int):
+        super().__init__()
+        self.mixer = IndependentVacancyField(dim, backend, field_chunk, triton_block_c, triton_chunk_t)
+        self.ff_norm = RMSNorm(dim)
+        self.ff = PackedSwiGLU(dim, hidden=ff_hidden)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        x = self.mixer(x)
+        return x + self.ff(self.ff_norm(x))
+
+    def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
+                ) -> Tuple[torch.Tensor, torch.Tensor]:
+        x, state = self.mixer.prefill(x, state)
+        return x + self.ff(self.ff_norm(x)), state
+
+    def step(self, x_t: torch.Tensor, state: torch.Tensor, params=None) -> torch.Tensor:
+        x_t = self.mixer.step(x_t, state, params)
+        return x_t + self.ff(self.ff_norm(x_t))
+
+
+class ScanPlan:
+    """Pre-bound ``fl_scan_forward`` call for a fixed raw tensor: output, state and workspace are
+    allocated once, so :meth:`run` is one C call (no allocation; capturable in a HIP graph).
+
+    ``raw`` may be refilled in place between runs; ``read`` and ``state_out`` are overwritten.
+    """
+
+    def __init__(self, raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+                 gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
+                 algo: int = nat.FL_ALGO_AUTO):
+        self.lib = nat.load()
+        batch, length, channels = _check_scan_inputs(raw, transition_r)
+        if raw.stride(2) != 1:
+            raise ValueError("raw must have channel stride 1")
+        if batch == 0 or length == 0 or channels == 0:
+            raise ValueError("ScanPlan needs a non-empty raw tensor")
+        dev = raw.device
+        self.raw = raw
+        self.params = [t.detach().to(device=dev, dtype=torch.float32).contiguous()
+                       for t in (transition_r, transition_i, gamma)]
+        self.state_in = None if state_in is None else state_in.detach().float().contiguous()
+        self.read = torch.empty((batch, length, 4 * channels), device=dev, dtype=torch.float32)
+        self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
+        self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
+        self.workspace = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+        self.args = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
+                     raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
+                     nat.ptr(self.state_out), nat.ptr(self.read), nat.FL_DTYPE_F32,
+                     nat.ptr(self.workspace), self.ws_bytes, algo)
+        self.device = dev
+
+    def run(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        code = self.lib.fl_scan_forward_ex(*self.args, ctypes.c_void_p(s.cuda_stream))
+        nat.check(code, "fl_scan_forward")
+        return self.read

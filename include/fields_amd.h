@@ -1,0 +1,109 @@
+/*
+ * fields_amd.h — C ABI of the MI355X (gfx950) Field-block hot path.
+ *
+ * The Field recurrence of Fields LM, per (batch b, time t, channel c), C = d_model / 2:
+ *
+ *   inj   = tanh(raw[b,t,c]) + i*tanh(raw[b,t,C+c])
+ *   v     = 0.9 * sigmoid(raw[b,t,2C+c])              (independent vacancy)
+ *   lam   = tr[c] + i*ti[c]
+ *   disp  = v * lam * s[t-1]                          (displaced readout)
+ *   s[t]  = (1 - v) * lam * s[t-1] + gamma[c]*v*inj   (causal write), s[-1] = state_in or 0
+ *   read[b,t,:] = [Re s | Im s | Re disp | Im disp]   (4C floats)
+ *
+ * All pointers are device pointers unless stated. Every entry point is stream-ordered on
+ * `stream`, performs no allocation and no host synchronisation (so a caller may capture it
+ * in a hipGraph), keeps no global mutable state and is reentrant: calls on different
+ * streams must use different workspaces.
+ *
+ * Complex state vectors are stored planar, [B, 2C] floats: the first C entries of a row
+ * are the real parts and the next C the imaginary parts (the layout of read[:, t, :2C]).
+ *
+ * Return value: FL_OK or one of the FL_ERR_* codes below. FL_ERR_HIP_BASE + e means that
+ * HIP reported error e (a hipError_t) on launch.
+ */
+#ifndef FIELDS_AMD_H_
+#define FIELDS_AMD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of raw / read buffers */
+#define FL_DTYPE_F32 0
+#define FL_DTYPE_BF16 1
+
+/* algorithm selector for fl_scan_forward_ex */
+#define FL_ALGO_AUTO 0
+#define FL_ALGO_CHUNKED3 1 /* chunk summary -> chunk carry -> chunk materialise (three launches) */
+
+#define FL_OK 0
+#define FL_ERR_INVALID_ARGUMENT 1 /* shape / stride / pointer check failed (Python: ValueError) */
+#define FL_ERR_DTYPE 2            /* unsupported raw or read dtype (Python: TypeError) */
+#define FL_ERR_WORKSPACE 3        /* workspace NULL or smaller than fl_scan_workspace_bytes */
+#define FL_ERR_HIP_BASE 1000      /* FL_ERR_HIP_BASE + hipError_t */
+
+/*
+ * Chunked forward scan over a whole sequence batch.
+ *
+ * Replaces `fused_field_read(raw, transition_r, transition_i, gamma, block_c, chunk_t)`
+ * (src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py:1108-1123) and the
+ * three Triton launches of `_ChunkedFieldReadFunction.forward` (same file, 913-1018:
+ * `_field_chunk_summary_kernel` 443-516, `_field_chunk_carry_kernel` 519-550,
+ * `_field_chunk_materialize_kernel` 553-622). The reference always starts from state 0 and
+ * takes fp32 raw only; state_in/state_out and bf16 raw are extensions (state_in = NULL and
+ * fp32 raw reproduce the reference call).
+ *
+ *   raw        [B, T, 3C] of raw_dtype; element (b,t,j) at raw + b*raw_stride_b + t*raw_stride_t + j
+ *              (strides in elements, channel stride 1, raw_stride_t >= 3C)
+ *   tr, ti, gamma  [C] fp32
+ *   state_in   [B, 2C] fp32 planar, or NULL for the zero state
+ *   state_out  [B, 2C] fp32 planar, or NULL; receives s[T-1]
+ *   read       [B, T, 4C] contiguous, read_dtype (FL_DTYPE_F32 only for now)
+ *   workspace  device scratch of at least fl_scan_workspace_bytes(B, T, C) bytes
+ */
+int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                    int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
+                    const float* gamma, const float* state_in, float* state_out, void* read,
+                    int read_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/* As fl_scan_forward with an explicit algorithm (FL_ALGO_*). */
+int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                       int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                       const float* ti, const float* gamma, const float* state_in,
+                       float* state_out, void* read, int read_dtype, void* workspace,
+                       size_t workspace_bytes, int algo, void* stream);
+
+/*
+ * Workspace size in bytes for fl_scan_forward at this shape (host function, no device call).
+ * Replaces the six [B, n_chunks, C] fp32 torch.empty buffers of
+ * field_only_v4_chunked_triton_wiki100.py:941-952.
+ */
+size_t fl_scan_workspace_bytes(int64_t B, int64_t T, int64_t C);
+
+/*
+ * Single-token recurrent step for the decode loop: reads state (s[t-1]) and raw_t, writes
+ * read_t and overwrites state with s[t], in one pass.
+ *
+ * The reference has no incremental step; this is the per-t body of
+ * `_field_chunk_materialize_kernel` (field_only_v4_chunked_triton_wiki100.py:583-621) applied
+ * to one token with the state carried between calls. Equal to row t of fl_scan_forward.
+ *
+ *   raw_t  [B, 3C] of raw_dtype, row stride raw_stride_b elements (>= 3C), channel stride 1
+ *   state  [B, 2C] fp32 planar, updated in place
+ *   read_t [B, 4C] contiguous, read_dtype (FL_DTYPE_F32 only for now)
+ */
+int fl_decode_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C, int64_t raw_stride_b,
+                   const float* tr, const float* ti, const float* gamma, float* state,
+                   void* read_t, int read_dtype, void* stream);
+
+/* Library version string (host function). No counterpart in the reference. */
+const char* fl_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FIELDS_AMD_H_ */

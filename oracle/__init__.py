@@ -1,0 +1,120 @@
+"""TEST INFRASTRUCTURE ONLY — the CPU oracle of the Field recurrence.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+this package, and only as the checker (or the timed CPU baseline), never as the measured or
+shipped path. The product (``fields_lm_amd``) never imports it.
+
+Contents
+--------
+* :func:`scan_f64` / :func:`decode_step_f64` — float64 sequential recurrence in plain C
+  (``field_oracle.c``), following ``reference_field_read``
+  (src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py:392-416).
+* :mod:`oracle.reference_path` — op-for-op torch restatement of the reference's CPU path
+  (``assoc_scan`` / ``hierarchical_scan`` / ``reference_field_read``, same file 333-416) and of
+  the Field mixer / block forward (1131-1221, 300-325). Also the timed CPU baseline.
+
+Pinning (tests/test_oracle.py): closed forms (T = 1, scipy.signal.lfilter for constant
+vacancy, geometric series), invariants (chunk-size independence, state continuation,
+``s_t + disp_t = lam*s_{t-1} + b_t``, causality), the two restatements against each other, and
+the golden fixtures of tests/golden/ written from the reference's own CPU path.
+"""
+from __future__ import annotations
+
+import ctypes
+import subprocess
+from pathlib import Path
+from typing import Optional, Tuple
+
+import numpy as np
+
+ORACLE_DIR = Path(__file__).resolve().parent
+C_SOURCE = ORACLE_DIR / "field_oracle.c"
+LIB_PATH = ORACLE_DIR / "_build" / "libfield_oracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile field_oracle.c with gcc into oracle/_build/libfield_oracle.so."""
+    LIB_PATH.parent.mkdir(parents=True, exist_ok=True)
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = ["gcc", "-O2", "-fPIC", "-shared", "-fno-fast-math", str(C_SOURCE), "-o", str(tmp), "-lm"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"gcc failed:\n{proc.stdout}\n{proc.stderr}")
+    tmp.replace(LIB_PATH)
+    return LIB_PATH
+
+
+def _load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists() or LIB_PATH.stat().st_mtime < C_SOURCE.stat().st_mtime:
+        build()
+    lib = ctypes.CDLL(str(LIB_PATH))
+    dp = ctypes.POINTER(ctypes.c_double)
+    i64 = ctypes.c_int64
+    lib.fo_scan_f64.argtypes = [dp, i64, i64, i64, i64, i64, dp, dp, dp, dp, dp, dp]
+    lib.fo_scan_f64.restype = None
+    lib.fo_decode_step_f64.argtypes = [dp, i64, i64, i64, dp, dp, dp, dp, dp]
+    lib.fo_decode_step_f64.restype = None
+    _lib = lib
+    return lib
+
+
+def _ptr(a: Optional[np.ndarray]):
+    if a is None:
+        return None
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_double))
+
+
+def _f64(a) -> np.ndarray:
+    if hasattr(a, "detach"):  # torch tensor
+        a = a.detach().to("cpu").double().numpy()
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float64))
+
+
+def scan_f64(raw, tr, ti, gamma, state_in=None) -> Tuple[np.ndarray, np.ndarray]:
+    """Sequential float64 Field scan.
+
+    raw [B,T,3C]; tr/ti/gamma [C]; state_in [B,2C] planar (re | im) or None.
+    Returns (read [B,T,4C], state_out [B,2C]) as float64 arrays.
+    """
+    lib = _load()
+    raw = _f64(raw)
+    if raw.ndim != 3 or raw.shape[2] % 3:
+        raise ValueError(f"raw must be [B,T,3C], got {raw.shape}")
+    B, T, C3 = raw.shape
+    C = C3 // 3
+    tr, ti, gamma = _f64(tr), _f64(ti), _f64(gamma)
+    if tr.shape != (C,) or ti.shape != (C,) or gamma.shape != (C,):
+        raise ValueError("tr/ti/gamma must be [C]")
+    sin = None if state_in is None else _f64(state_in).reshape(B, 2 * C)
+    read = np.empty((B, T, 4 * C), dtype=np.float64)
+    sout = np.empty((B, 2 * C), dtype=np.float64)
+    lib.fo_scan_f64(_ptr(raw), B, T, C, T * C3, C3, _ptr(tr), _ptr(ti), _ptr(gamma), _ptr(sin),
+                    _ptr(sout), _ptr(read))
+    return read, sout
+
+
+def decode_step_f64(raw_t, tr, ti, gamma, state) -> Tuple[np.ndarray, np.ndarray]:
+    """One float64 decode step. raw_t [B,3C], state [B,2C] planar. Returns (read_t, new_state)."""
+    lib = _load()
+    raw_t = _f64(raw_t)
+    B, C3 = raw_t.shape
+    C = C3 // 3
+    st = _f64(state).reshape(B, 2 * C).copy()
+    out = np.empty((B, 4 * C), dtype=np.float64)
+    lib.fo_decode_step_f64(_ptr(raw_t), B, C, C3, _ptr(_f64(tr)), _ptr(_f64(ti)), _ptr(_f64(gamma)),
+                           _ptr(st), _ptr(out))
+    return out, st
+
+
+def rel_err(actual, expected) -> float:
+    """Norm-wise relative error max|actual - expected| / max|expected| (the parity metric)."""
+    a = _f64(actual)
+    e = _f64(expected)
+    denom = float(np.max(np.abs(e))) if e.size else 0.0
+    diff = float(np.max(np.abs(a - e))) if e.size else 0.0
+    return diff / max(denom, 1e-30)

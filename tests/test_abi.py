@@ -1,0 +1,107 @@
+"""C-ABI library: loads, exports every symbol include/fields_amd.h declares, host-side checks.
+
+No kernel is launched here (no GPU in the build container): only host functions and argument
+validation paths that return before any HIP call.
+"""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from fields_lm_amd import _native as nat
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "fields_amd.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fl_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not nat.LIB_PATH.exists():
+        from fields_lm_amd import build
+
+        build.build()
+    return nat.load()
+
+
+def test_header_declares_expected_entry_points():
+    names = _declared_functions()
+    assert {"fl_scan_forward", "fl_scan_forward_ex", "fl_scan_workspace_bytes",
+            "fl_decode_step", "fl_version"} <= set(names)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+        assert name in nat.SIGNATURES, name
+
+
+def test_header_constants_match_binding():
+    text = HEADER.read_text()
+    consts = dict(re.findall(r"#define (FL_[A-Z0-9_]+) (\d+)", text))
+    for name, value in consts.items():
+        assert getattr(nat, name) == int(value), name
+
+
+def test_version_and_workspace_size(lib):
+    assert lib.fl_version().decode().startswith("fields_amd")
+    n_chunks = (2048 + 63) // 64
+    assert lib.fl_scan_workspace_bytes(8, 2048, 512) == 8 * n_chunks * 512 * 24 + 256
+    assert lib.fl_scan_workspace_bytes(0, 2048, 512) == 0
+    assert lib.fl_scan_workspace_bytes(1, 65536, 512) == 1024 * 512 * 24 + 256
+
+
+def _scan(lib, **kw):
+    a = dict(raw=16, raw_dtype=0, B=1, T=4, C=8, sb=4 * 24, st=24, tr=16, ti=16, gamma=16,
+             state_in=None, state_out=None, read=16, read_dtype=0, ws=16, ws_bytes=1 << 20,
+             algo=0, stream=None)
+    a.update(kw)
+    return lib.fl_scan_forward_ex(a["raw"], a["raw_dtype"], a["B"], a["T"], a["C"], a["sb"], a["st"],
+                                  a["tr"], a["ti"], a["gamma"], a["state_in"], a["state_out"], a["read"],
+                                  a["read_dtype"], a["ws"], a["ws_bytes"], a["algo"], a["stream"])
+
+
+def test_argument_validation_returns_before_launch(lib):
+    # fake (never dereferenced) pointers: every case below fails validation first
+    assert _scan(lib, raw_dtype=7) == nat.FL_ERR_DTYPE
+    assert _scan(lib, read_dtype=1) == nat.FL_ERR_DTYPE
+    assert _scan(lib, B=0) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, T=-1) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, st=23) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, B=2, sb=24) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, raw=None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, read=None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, algo=9) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, ws=None) == nat.FL_ERR_WORKSPACE
+    assert _scan(lib, ws_bytes=10) == nat.FL_ERR_WORKSPACE
+    assert _scan(lib, raw=17) == nat.FL_ERR_INVALID_ARGUMENT  # misaligned bf16/f32 pointer
+    assert lib.fl_decode_step(16, 3, 1, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_DTYPE
+    assert lib.fl_decode_step(16, 0, 0, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert lib.fl_decode_step(16, 0, 1, 8, 23, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert lib.fl_decode_step(None, 0, 1, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+
+
+def test_error_mapping():
+    nat.check(nat.FL_OK, "x")
+    with pytest.raises(ValueError):
+        nat.check(nat.FL_ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(TypeError):
+        nat.check(nat.FL_ERR_DTYPE, "x")
+    with pytest.raises(RuntimeError):
+        nat.check(nat.FL_ERR_WORKSPACE, "x")
+    with pytest.raises(RuntimeError, match="HIP error 2"):
+        nat.check(nat.FL_ERR_HIP_BASE + 2, "x")
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(nat, "_lib", None)
+    monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        nat.load()

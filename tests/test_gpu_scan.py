@@ -1,0 +1,313 @@
+"""GPU parity of the HIP Field scan / decode step against the CPU oracle (float64 C).
+
+Tolerance: norm-wise relative error max|hip - oracle| / max|oracle| <= 1e-4 for the scan and
+decode kernels (fp32 state; bf16 raw is upcast exactly, so the same bound holds), <= 2e-2 for
+the whole bf16 block under autocast (bf16 GEMMs), as stated for this path.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+TOL_BF16_BLOCK = 2e-2
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from fields_lm_amd import _native
+
+    _native.load()
+    return torch.device("cuda:0")
+
+
+def _params(C, seed):
+    rl, th = ref.init_radius_theta(C)
+    g = torch.Generator().manual_seed(seed)
+    rl = rl + 0.5 * torch.randn(C, generator=g)
+    th = th + 0.3 * torch.randn(C, generator=g)
+    return ref.transition_params(rl, th)
+
+
+def _to(dev, *ts):
+    return [t.to(dev).contiguous() for t in ts]
+
+
+SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
+          (4, 257, 512), (2, 1000, 1024)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_scan_matches_oracle(dev, shape, dtype):
+    from fields_lm_amd import field_scan
+
+    B, T, C = shape
+    print(f"[case] scan shape={shape} dtype={dtype}", flush=True)
+    g = torch.Generator().manual_seed(B * 1000 + T + C)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+    tr, ti, gamma = _params(C, seed=C)
+    read, state = field_scan(*_to(dev, raw, tr, ti, gamma), return_state=True)
+    torch.cuda.synchronize()
+    exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma)
+    assert oracle.rel_err(read.cpu(), exp_read) <= TOL
+    assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+    assert torch.isfinite(read).all()
+
+
+def test_scan_state_in_continuation(dev):
+    from fields_lm_amd import field_scan
+
+    B, T, C, cut = 3, 300, 96, 131
+    print("[case] state continuation", flush=True)
+    g = torch.Generator().manual_seed(11)
+    raw = torch.randn(B, T, 3 * C, generator=g)
+    tr, ti, gamma = _params(C, 11)
+    draw, dtr, dti, dgm = _to(dev, raw, tr, ti, gamma)
+    head, s1 = field_scan(draw[:, :cut], dtr, dti, dgm, return_state=True)
+    tail, s2 = field_scan(draw[:, cut:], dtr, dti, dgm, state_in=s1, return_state=True)
+    exp_read, exp_state = oracle.scan_f64(raw, tr, ti, gamma)
+    assert oracle.rel_err(torch.cat([head, tail], 1).cpu(), exp_read) <= TOL
+    assert oracle.rel_err(s2.cpu(), exp_state) <= TOL
+    # a nonzero state_in against the oracle directly
+    sin = torch.randn(B, 2 * C, generator=g) * 0.3
+    r3, s3 = field_scan(draw, dtr, dti, dgm, state_in=sin.to(dev), return_state=True)
+    e_read, e_state = oracle.scan_f64(raw, tr, ti, gamma, state_in=sin)
+    assert oracle.rel_err(r3.cpu(), e_read) <= TOL
+    assert oracle.rel_err(s3.cpu(), e_state) <= TOL
+
+
+def test_scan_strided_raw(dev):
+    """raw as a view: padded time stride (column slice) and a strided batch dimension."""
+    from fields_lm_amd import field_scan
+
+    B, T, C = 4, 77, 64
+    print("[case] strided raw", flush=True)
+    g = torch.Generator().manual_seed(12)
+    big = torch.randn(2 * B, T, 3 * C + 8, generator=g)
+    view_cpu = big[::2, :, :3 * C]
+    tr, ti, gamma = _params(C, 12)
+    dbig = big.to(dev)
+    view = dbig[::2, :, :3 * C]
+    assert view.stride(1) == 3 * C + 8 and view.stride(2) == 1
+    read = field_scan(view, *_to(dev, tr, ti, gamma))
+    exp_read, _ = oracle.scan_f64(view_cpu.contiguous(), tr, ti, gamma)
+    assert oracle.rel_err(read.cpu(), exp_read) <= TOL
+
+
+def test_empty_and_errors(dev):
+    from fields_lm_amd import field_scan, fused_field_read
+
+    C = 16
+    tr, ti, gamma = _to(dev, *_params(C, 1))
+    read, state = field_scan(torch.zeros(2, 0, 3 * C, device=dev), tr, ti, gamma, return_state=True)
+    assert read.shape == (2, 0, 4 * C)
+    assert torch.count_nonzero(state) == 0
+    with pytest.raises(TypeError):
+        fused_field_read(torch.zeros(1, 4, 3 * C, device=dev, dtype=torch.float16), tr, ti, gamma, 32, 64)
+    with pytest.raises(ValueError):
+        fused_field_read(torch.zeros(1, 4, 3 * C + 1, device=dev), tr, ti, gamma, 32, 64)
+    with pytest.raises(ValueError):
+        fused_field_read(torch.zeros(1, 4, 3 * (C + 1), device=dev), tr, ti, gamma, 32, 64)
+
+
+@pytest.mark.parametrize("name", ["scan_b8_t2048_d1024", "scan_b1_t65536_d1024"])
+def test_full_size_workloads(dev, name):
+    """Configs 2 and 4 at full size, bf16 raw; config 4 also checks the carry at every
+    2,048-step boundary (32 boundaries) against float64."""
+    from fields_lm_amd import field_scan
+    from fields_lm_amd.workloads import make_scan_workload
+
+    print(f"[case] full size {name}", flush=True)
+    wl = make_scan_workload(name, dev)
+    read, state = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma, return_state=True)
+    torch.cuda.synchronize()
+    exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
+    got = read.cpu()
+    assert oracle.rel_err(got, exp_read) <= TOL
+    assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+    T = wl.raw.shape[1]
+    C = wl.channels
+    for t in range(2047, T, 2048):
+        assert oracle.rel_err(got[:, t, :2 * C], exp_read[:, t, :2 * C]) <= TOL, t
+    del exp_read
+
+
+def test_fp32_raw_config2_shape(dev):
+    from fields_lm_amd import field_scan
+    from fields_lm_amd.workloads import make_scan_workload
+
+    print("[case] config2 fp32 raw", flush=True)
+    wl = make_scan_workload("scan_b8_t2048_d1024", dev, dtype=torch.float32)
+    read = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma)
+    exp_read, _ = oracle.scan_f64(wl.raw.cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
+    assert oracle.rel_err(read.cpu(), exp_read) <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# decode step
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("C", [32, 5, 512])
+def test_decode_steps_reproduce_scan(dev, C, dtype):
+    from fields_lm_amd import field_decode_step, field_scan
+
+    B, T = 3, 45
+    print(f"[case] decode C={C} dtype={dtype}", flush=True)
+    g = torch.Generator().manual_seed(C)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+    tr, ti, gamma = _params(C, C)
+    draw, dtr, dti, dgm = _to(dev, raw, tr, ti, gamma)
+    full = field_scan(draw, dtr, dti, dgm)
+    state = torch.zeros(B, 2 * C, device=dev)
+    rows = [field_decode_step(draw[:, t], dtr, dti, dgm, state) for t in range(T)]
+    steps = torch.stack(rows, 1)
+    exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma)
+    assert oracle.rel_err(steps.cpu(), exp_read) <= TOL
+    assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+    assert oracle.rel_err(steps.cpu(), full.cpu()) <= TOL
+
+
+def test_decode_b64_against_oracle_step(dev):
+    from fields_lm_amd import field_decode_step
+
+    B, C = 64, 512
+    print("[case] decode B64", flush=True)
+    g = torch.Generator().manual_seed(64)
+    raw_t = torch.randn(B, 3 * C, generator=g).to(torch.bfloat16)
+    state = torch.randn(B, 2 * C, generator=g) * 0.5
+    tr, ti, gamma = _params(C, 64)
+    dstate = state.to(dev)
+    out = field_decode_step(*_to(dev, raw_t, tr, ti, gamma), dstate)
+    exp_out, exp_state = oracle.decode_step_f64(raw_t.float(), tr, ti, gamma, state)
+    assert oracle.rel_err(out.cpu(), exp_out) <= TOL
+    assert oracle.rel_err(dstate.cpu(), exp_state) <= TOL
+
+
+def test_decode_step_in_hip_graph(dev):
+    """The decode step captured in a HIP graph: every replay equals the eager step."""
+    from fields_lm_amd import field_decode_step
+
+    B, C = 64, 512
+    print("[case] decode hipGraph", flush=True)
+    g = torch.Generator().manual_seed(5)
+    tr, ti, gamma = _to(dev, *_params(C, 5))
+    raw_buf = torch.zeros(B, 3 * C, device=dev, dtype=torch.bfloat16)
+    state = torch.zeros(B, 2 * C, device=dev)
+    out = torch.empty(B, 4 * C, device=dev)
+    # warm up outside capture
+    field_decode_step(raw_buf, tr, ti, gamma, state, out=out)
+    state.zero_()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        field_decode_step(raw_buf, tr, ti, gamma, state, out=out)
+    torch.cuda.synchronize()
+    state.zero_()
+    eager_state = torch.zeros(B, 2 * C, device=dev)
+    for _ in range(6):
+        raw_t = (torch.randn(B, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+        raw_buf.copy_(raw_t)
+        graph.replay()
+        torch.cuda.synchronize()
+        eager_out = field_decode_step(raw_t, tr, ti, gamma, eager_state)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(out, eager_out, rtol=0, atol=0)
+        torch.testing.assert_close(state, eager_state, rtol=0, atol=0)
+
+
+# ---------------------------------------------------------------------------------------------
+# Field block (drop-in module) against the reference's golden vectors
+# ---------------------------------------------------------------------------------------------
+
+def _golden_block(golden_dir):
+    from fields_lm_amd import FieldBlock
+
+    d = np.load(golden_dir / "selftest_block.npz")
+    sd = {k[len("param::"):]: torch.from_numpy(d[k]) for k in d.files if k.startswith("param::")}
+    block = FieldBlock(64, "triton", 8, 8, 16, 192)
+    block.load_state_dict(sd, strict=True)
+    return block, d
+
+
+def test_block_fp32_matches_reference_golden(dev, golden_dir):
+    block, d = _golden_block(golden_dir)
+    print("[case] block fp32 golden", flush=True)
+    block = block.to(dev)
+    rec = {}
+    h = block.mixer.read_norm.register_forward_pre_hook(lambda m, i: rec.__setitem__("read", i[0].detach()))
+    with torch.no_grad():
+        out = block(torch.from_numpy(d["x"]).to(dev))
+    h.remove()
+    assert oracle.rel_err(rec["read"].cpu(), d["read"]) <= TOL
+    assert oracle.rel_err(out.cpu(), d["block_out"]) <= TOL
+    with torch.no_grad():
+        mix = block.mixer(torch.from_numpy(d["x"]).to(dev))
+    assert oracle.rel_err(mix.cpu(), d["mixer_out"]) <= TOL
+
+
+def test_block_bf16_autocast_matches_reference_golden(dev, golden_dir):
+    block, _ = _golden_block(golden_dir)
+    d = np.load(golden_dir / "selftest_block_bf16.npz")
+    print("[case] block bf16 golden", flush=True)
+    block = block.to(device=dev, dtype=torch.bfloat16)
+    x = torch.from_numpy(d["x"]).to(device=dev, dtype=torch.bfloat16)
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        out = block(x)
+    assert out.dtype == torch.bfloat16
+    assert oracle.rel_err(out.float().cpu(), d["block_out"]) <= TOL_BF16_BLOCK
+
+
+def test_config1_block_rows_match_reference_golden(dev, golden_dir):
+    """Config 1: promoted-geometry block, seed 0, fp32, B=1 T=2048 d=1024 — output rows and the
+    final complex state against the reference's CPU path."""
+    from fields_lm_amd import FieldBlock
+
+    d = np.load(golden_dir / "config1_block.npz")
+    print("[case] config1 block golden", flush=True)
+    torch.manual_seed(0)
+    block = FieldBlock(1024, "triton", 32, 32, 64, 2752)
+    x = torch.randn(1, 2048, 1024)
+    block = block.to(dev)
+    rows = torch.from_numpy(d["rows"])
+    with torch.no_grad():
+        y, state = block.prefill(x.to(dev))
+    y = y.cpu()
+    assert oracle.rel_err(y[0, rows], d["block_rows"]) <= TOL
+    assert oracle.rel_err(state[0].cpu(), d["final_state"].reshape(-1)) <= TOL
+
+
+def test_block_prefill_then_steps_equal_forward(dev):
+    from fields_lm_amd import FieldBlock
+
+    print("[case] block prefill+step", flush=True)
+    torch.manual_seed(3)
+    block = FieldBlock(256, "triton", 32, 32, 64, 512).to(dev)
+    x = torch.randn(2, 50, 256, device=dev)
+    with torch.no_grad():
+        full = block(x)
+        y, state = block.prefill(x[:, :40])
+        params = block.mixer.transition()
+        steps = [block.step(x[:, t], state, params) for t in range(40, 50)]
+    assert oracle.rel_err(y.cpu(), full[:, :40].cpu()) <= TOL
+    assert oracle.rel_err(torch.stack(steps, 1).cpu(), full[:, 40:].cpu()) <= TOL
+
+
+def test_block_causality(dev):
+    """canon:1456-1461: prefix 23 of 37 gives the same outputs (tolerance 2e-4 there)."""
+    block, d = _golden_block(golden_dir=__import__("pathlib").Path(__file__).parent / "golden")
+    block = block.to(dev)
+    x = torch.from_numpy(d["x"]).to(dev)
+    with torch.no_grad():
+        full = block(x)
+        pre = block(x[:, :23].contiguous())
+    assert float((full[:, :23] - pre).abs().max()) <= 2e-4
