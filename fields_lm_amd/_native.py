@@ -20,6 +20,7 @@ FL_DTYPE_F32 = 0
 FL_DTYPE_BF16 = 1
 FL_ALGO_AUTO = 0
 FL_ALGO_CHUNKED3 = 1
+FL_ALGO_LOOKBACK = 2
 FL_OK = 0
 FL_ERR_INVALID_ARGUMENT = 1
 FL_ERR_DTYPE = 2
@@ -95,3 +96,24 @@ def ptr(t):
 
 def stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+# Scan workspaces, one per (device, stream): zero-filled when allocated, then reused as is
+# (the library keeps a launch counter in the first 256 bytes and re-arms it after every call).
+_workspaces: dict = {}
+
+
+def scan_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """Zero-filled, 256-byte aligned workspace of at least ``nbytes`` for the current stream."""
+    stream = torch.cuda.current_stream(device)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
+        _workspaces[key] = ws
+    return ws
+
+
+def workspace_error(ws: torch.Tensor) -> int:
+    """Error word of a scan workspace header (0 = every look-back wait completed)."""
+    return int(ws[12:16].view(torch.int32).item())

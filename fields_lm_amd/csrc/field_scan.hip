@@ -2,23 +2,25 @@
 //
 // Path (reference: src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py,
 // cited below as "canon"):
-//   fused_field_read                      canon:1108-1123  -> fl_scan_forward
-//   _field_chunk_summary_kernel           canon:443-516    -> fl_chunk_summary_kernel
-//   _field_chunk_carry_kernel             canon:519-550    -> fl_chunk_carry_kernel
-//   _field_chunk_materialize_kernel       canon:553-622    -> fl_chunk_materialize_kernel
-//   (no reference counterpart)                             -> fl_decode_step_kernel
+//   fused_field_read                  canon:1108-1123  -> fl_scan_forward
+//   _field_chunk_summary_kernel       canon:443-516    -> fl_chunk_summary_kernel / look-back kernel
+//   _field_chunk_carry_kernel         canon:519-550    -> fl_chunk_carry_kernel / look-back
+//   _field_chunk_materialize_kernel   canon:553-622    -> fl_chunk_materialize_kernel / look-back kernel
+//   (no reference counterpart)                         -> fl_decode_step_kernel
 //
 // Work decomposition (MI355X: 64-lane waves, 256 CUs in 8 XCDs, HBM3E):
-//   * lane  <-> K adjacent channels, so one wave-wide load of a raw segment is a single
-//     64*K-element contiguous run (512 B for bf16 K=4) and one store of a read segment is
-//     64*K*4 contiguous bytes;
-//   * wave  <-> L consecutive time steps of the chunk, processed sequentially per lane;
-//   * block <-> (batch row, channel tile of 64*K channels, time chunk of W*L = kChunkT steps).
-// The time-parallel prefix inside a chunk runs across the W waves through LDS (one affine
-// summary per wave), the prefix across chunks runs in fl_chunk_carry_kernel.
+//   * lane  <-> K adjacent channels: one wave-wide load of a raw segment is a contiguous run of
+//     64*K elements and one store of a read segment is 64*K*4 contiguous bytes;
+//   * wave  <-> L consecutive time steps, processed sequentially per lane;
+//   * block <-> tile = (batch row, channel tile of 64*K channels, time chunk of W*L steps).
+// Raw is read and read is written through buffer instructions whose per-step offset is a
+// wave-uniform scalar (the per-lane VGPR offset is just the channel), so the address math costs
+// no vector instructions, and whose descriptor bounds make rows past T read as 0 and drop stores.
 //
-// The affine map of one step is s -> a*s + b with a = (1-v)*lam, b = gamma*v*inj (complex).
-// Chunk summaries compose these maps: (A,B) then (a,b) gives (a*A, a*B + b).
+// The affine map of one step is s -> a*s + b with a = (1-v)*lam and b = gamma*v*inj (complex).
+// Because lam is constant per channel, the map of n full steps is
+//   A = lam^n * prod(1 - v)   (a complex constant times a REAL product),   B = state from 0,
+// so a summary is (P, B) = (prod(1-v), B) and composing summaries only multiplies by lam^n.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stddef.h>
@@ -29,20 +31,103 @@ namespace {
 
 constexpr float kVacancyMax = 0.9f;  // canon:68 VAC_MAX
 constexpr float kLog2e = 1.4426950408889634f;
-constexpr int kChunkT = 64;      // time steps per chunk; every tiling below uses W*L == kChunkT
+constexpr int kChunkT = 64;      // chunk length of the three-phase path
 constexpr int kCarryWaves = 16;  // waves (chunk groups) per block in fl_chunk_carry_kernel
+constexpr uint32_t kBufDword3 = 0x00020000u;  // gfx9 raw-buffer descriptor word 3
 
 typedef unsigned short bf16_bits;
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           (int)kBufDword3);
+}
+
+__device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
 // ------------------------------------------------------------------------------------------
-// element loads: K adjacent channels as fp32
+// element access: K adjacent channels, as fp32
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
+// raw: buffer load at (voffset, soffset) bytes
 template <typename RawT, int K>
-struct Load;
+struct RawLoad;
+template <>
+struct RawLoad<float, 1> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    o[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+  }
+};
+template <>
+struct RawLoad<float, 2> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
+  }
+};
+template <>
+struct RawLoad<float, 4> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
+    o[2] = __uint_as_float(w.z); o[3] = __uint_as_float(w.w);
+  }
+};
+template <>
+struct RawLoad<bf16_bits, 1> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    o[0] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0) << 16);
+  }
+};
+template <>
+struct RawLoad<bf16_bits, 2> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
+    o[0] = bf16_lo(w); o[1] = bf16_hi(w);
+  }
+};
+template <>
+struct RawLoad<bf16_bits, 4> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x); o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
+  }
+};
 
+// read: buffer store of K floats
+template <int K>
+struct ReadStore;
+template <>
+struct ReadStore<1> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, 0);
+  }
+};
+template <>
+struct ReadStore<2> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    u32x2 w;
+    w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, 0);
+  }
+};
+template <>
+struct ReadStore<4> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    u32x4 w;
+    w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
+    w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, vo, so, 0);
+  }
+};
+
+// plain pointer access (decode step, carry planes)
+template <typename T, int K>
+struct Load;
 template <>
 struct Load<float, 1> {
   __device__ __forceinline__ static void run(const float* p, float* o) { o[0] = p[0]; }
@@ -102,35 +187,171 @@ struct Store<4> {
 };
 
 // ------------------------------------------------------------------------------------------
-// gates (canon:487-505, 599-615): tanh written as 1 - 2/(1+e^{2x}) (= 2*sigmoid(2x) - 1),
-// sigmoid as 1/(1+e^{-x}); exp via v_exp_f32 (2^x), reciprocal via v_rcp_f32.
+// gates (canon:399-406; the Triton form canon:487-505, 599-615)
+//   inj = tanh(zr) + i tanh(zi),   v = 0.9 * sigmoid(zv),   b = gamma * v * inj
+// tanh(x) = sign(x) (1-u)/(1+u) with u = e^{-2|x|} in (0,1]: both denominators lie in [1,2],
+// so one v_rcp_f32 of their product serves both. sigmoid(z) = 1/(1+e^{-z}) with its own
+// v_rcp_f32 (rcp(inf) = 0 gives sigmoid(-inf) = 0). No clamps; NaN propagates.
+// exp is v_exp_f32 (2^x) on pre-scaled arguments.
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ void gates(float zr, float zi, float zv, float gm, float& v,
                                       float& br, float& bi) {
-  const float er = __builtin_amdgcn_exp2f(zr * (2.0f * kLog2e));
-  const float ei = __builtin_amdgcn_exp2f(zi * (2.0f * kLog2e));
-  const float ev = __builtin_amdgcn_exp2f(zv * -kLog2e);
-  const float inj_r = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + er);
-  const float inj_i = 1.0f - 2.0f * __builtin_amdgcn_rcpf(1.0f + ei);
-  v = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + ev);
+  const float ur = __builtin_amdgcn_exp2f(fabsf(zr) * (-2.0f * kLog2e));
+  const float ui = __builtin_amdgcn_exp2f(fabsf(zi) * (-2.0f * kLog2e));
+  const float dr = 1.0f + ur, di = 1.0f + ui;
+  const float rdi = __builtin_amdgcn_rcpf(dr * di);
+  const float tr_abs = (1.0f - ur) * (di * rdi);
+  const float ti_abs = (1.0f - ui) * (dr * rdi);
+  v = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv * -kLog2e));
   const float scale = gm * v;
-  br = scale * inj_r;
-  bi = scale * inj_i;
+  br = scale * copysignf(tr_abs, zr);
+  bi = scale * copysignf(ti_abs, zi);
 }
 
-// (A,B) <- step (a,b) applied after (A,B)
-__device__ __forceinline__ void compose(float ar, float ai, float br, float bi, float& Ar,
-                                        float& Ai, float& Br, float& Bi) {
-  const float nAr = ar * Ar - ai * Ai;
-  const float nAi = ar * Ai + ai * Ar;
-  const float nBr = ar * Br - ai * Bi + br;
-  const float nBi = ar * Bi + ai * Br + bi;
-  Ar = nAr; Ai = nAi; Br = nBr; Bi = nBi;
+// complex power lam^n by repeated squaring (n >= 0)
+__device__ __forceinline__ void cpow(float lr, float li, int n, float& pr, float& pi) {
+  float rr = 1.f, ri = 0.f, br = lr, bi = li;
+  while (n > 0) {
+    if (n & 1) {
+      const float t = rr * br - ri * bi;
+      ri = rr * bi + ri * br;
+      rr = t;
+    }
+    const float t = br * br - bi * bi;
+    bi = 2.f * br * bi;
+    br = t;
+    n >>= 1;
+  }
+  pr = rr; pi = ri;
+}
+
+// s <- A s + B with A = lamn * P (lamn complex, P real)
+__device__ __forceinline__ void apply_map(float lnr, float lni, float P, float Br, float Bi,
+                                          float& sr, float& si) {
+  const float mr = lnr * sr - lni * si;
+  const float mi = lnr * si + lni * sr;
+  sr = fmaf(P, mr, Br);
+  si = fmaf(P, mi, Bi);
 }
 
 // ------------------------------------------------------------------------------------------
-// Phase 1: per-chunk affine summary (A,B) of kChunkT steps.
-// agg layout [B][n_chunks][4][C]: planes Ar, Ai, Br, Bi.
+// wave tile: L steps x K channels per lane
+// ------------------------------------------------------------------------------------------
+template <typename RawT, int K, int L>
+struct WaveTile {
+  float gv[L][K], gbr[L][K], gbi[L][K];  // gates, kept between summary and materialisation
+
+  // Loads L rows from the raw descriptor (row j at soffset so0 + j*row_bytes) and forms gates.
+  // Rows past the descriptor's bound read as 0; their gates are never used.
+  __device__ __forceinline__ void load(rsrc_t r, int vo, int so0, int row_bytes, int plane_bytes,
+                                       const float* gm) {
+    float z[L][3][K];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const int so = so0 + j * row_bytes;
+      RawLoad<RawT, K>::run(r, vo, so, z[j][0]);
+      RawLoad<RawT, K>::run(r, vo, so + plane_bytes, z[j][1]);
+      RawLoad<RawT, K>::run(r, vo, so + 2 * plane_bytes, z[j][2]);
+    }
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+#pragma unroll
+      for (int k = 0; k < K; ++k)
+        gates(z[j][0][k], z[j][1][k], z[j][2][k], gm[k], gv[j][k], gbr[j][k], gbi[j][k]);
+    }
+  }
+
+  // Summary over all L steps: P = prod(1-v), B = state reached from 0.
+  __device__ __forceinline__ void summary(const float* lr, const float* li, float* P, float* Br,
+                                          float* Bi) const {
+#pragma unroll
+    for (int k = 0; k < K; ++k) { P[k] = 1.f; Br[k] = 0.f; Bi[k] = 0.f; }
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const float keep = 1.f - gv[j][k];
+        const float mr = lr[k] * Br[k] - li[k] * Bi[k];
+        const float mi = lr[k] * Bi[k] + li[k] * Br[k];
+        Br[k] = fmaf(keep, mr, gbr[j][k]);
+        Bi[k] = fmaf(keep, mi, gbi[j][k]);
+        P[k] *= keep;
+      }
+    }
+  }
+
+  // Recurrence from (sr, si) over the first n steps, storing
+  // read[b,t,:] = [Re s | Im s | Re disp | Im disp] (canon:583-621), row j at so0 + j*row_bytes.
+  __device__ __forceinline__ void materialize(rsrc_t w, int vo, int so0, int row_bytes,
+                                              int plane_bytes, int n, const float* lr,
+                                              const float* li, float* sr, float* si) const {
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      if (j < n) {
+        float dr[K], di[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          // m = lam*s_prev, disp = v*m, s = (1-v)*m + b
+          const float mr = lr[k] * sr[k] - li[k] * si[k];
+          const float mi = lr[k] * si[k] + li[k] * sr[k];
+          dr[k] = gv[j][k] * mr;
+          di[k] = gv[j][k] * mi;
+          sr[k] = (mr - dr[k]) + gbr[j][k];
+          si[k] = (mi - di[k]) + gbi[j][k];
+        }
+        const int so = so0 + j * row_bytes;
+        ReadStore<K>::run(w, vo, so, sr);
+        ReadStore<K>::run(w, vo, so + plane_bytes, si);
+        ReadStore<K>::run(w, vo, so + 2 * plane_bytes, dr);
+        ReadStore<K>::run(w, vo, so + 3 * plane_bytes, di);
+      }
+    }
+  }
+};
+
+template <int K>
+__device__ __forceinline__ void load_params(const float* __restrict__ tr, const float* __restrict__ ti,
+                                            const float* __restrict__ gamma, int c0, bool ok,
+                                            float* lr, float* li, float* gm) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    lr[k] = ok ? tr[c0 + k] : 0.f;
+    li[k] = ok ? ti[c0 + k] : 0.f;
+    gm[k] = ok ? gamma[c0 + k] : 0.f;
+  }
+}
+
+// Buffer descriptors of one tile: raw from row t_begin of batch row b to the end of row T-1,
+// read over the same rows.
+struct TileIo {
+  rsrc_t raw, read;
+  int vo_raw, vo_read;          // per-lane channel byte offsets
+  int raw_row, raw_plane;       // bytes between rows / between the 3 raw planes
+  int read_row, read_plane;     // bytes between rows / between the 4 read planes
+};
+
+template <typename RawT>
+__device__ __forceinline__ TileIo tile_io(const RawT* raw, int64_t sb, int64_t st, float* read,
+                                          int T, int C, int b, int t_begin, int c0) {
+  TileIo io;
+  const int rows = T - t_begin;  // >= 1
+  const RawT* rbase = raw + (int64_t)b * sb + (int64_t)t_begin * st;
+  io.raw = make_rsrc(rbase, (uint32_t)(((int64_t)(rows - 1) * st + 3 * (int64_t)C) * sizeof(RawT)));
+  float* wbase = read + ((int64_t)b * T + t_begin) * 4 * C;
+  io.read = make_rsrc(wbase, (uint32_t)((int64_t)rows * 4 * C * sizeof(float)));
+  io.vo_raw = c0 * (int)sizeof(RawT);
+  io.vo_read = c0 * (int)sizeof(float);
+  io.raw_row = (int)(st * (int64_t)sizeof(RawT));
+  io.raw_plane = C * (int)sizeof(RawT);
+  io.read_row = 4 * C * (int)sizeof(float);
+  io.read_plane = C * (int)sizeof(float);
+  return io;
+}
+
+// ------------------------------------------------------------------------------------------
+// Three-phase path (FL_ALGO_CHUNKED3), chunks of kChunkT = W*L steps.
+// Phase 1: per-chunk summary (P, B). agg layout [B][n_chunks][3][C]: P, Br, Bi. The last
+// chunk's summary is never consumed and is not computed.
 // ------------------------------------------------------------------------------------------
 template <typename RawT, int K, int L, int W>
 __global__ __launch_bounds__(W * 64) void fl_chunk_summary_kernel(
@@ -139,108 +360,83 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_summary_kernel(
     float* __restrict__ agg) {
   static_assert(W * L == kChunkT, "chunk length mismatch");
   constexpr int CT = 64 * K;
-  __shared__ float s_sum[W][4][CT];
+  __shared__ float s_sum[W][3][CT];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
   const int chunk = blockIdx.x;
+  if (chunk == n_chunks - 1) return;
   const int b = blockIdx.z;
   const int c0 = blockIdx.y * CT + lane * K;
   const bool ok = c0 < C;  // C % K == 0, so all K channels are in range together
 
   float lr[K], li[K], gm[K];
+  load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
+  const TileIo io = tile_io<RawT>(raw, sb, st, nullptr, T, C, b, chunk * kChunkT, c0);
+  WaveTile<RawT, K, L> tile;
+  tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
+  float P[K], Br[K], Bi[K];
+  tile.summary(lr, li, P, Br, Bi);
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    lr[k] = ok ? tr[c0 + k] : 0.f;
-    li[k] = ok ? ti[c0 + k] : 0.f;
-    gm[k] = ok ? gamma[c0 + k] : 0.f;
-  }
-
-  const int t0 = chunk * kChunkT + wave * L;
-  const RawT* base = raw + (int64_t)b * sb + c0;
-  float z[L][3][K];
-#pragma unroll
-  for (int j = 0; j < L; ++j) {
-    const int t = t0 + j;
-    if (ok && t < T) {
-      const RawT* p = base + (int64_t)t * st;
-      Load<RawT, K>::run(p, z[j][0]);
-      Load<RawT, K>::run(p + C, z[j][1]);
-      Load<RawT, K>::run(p + 2 * C, z[j][2]);
-    } else {
-#pragma unroll
-      for (int k = 0; k < K; ++k) z[j][0][k] = z[j][1][k] = z[j][2][k] = 0.f;
-    }
-  }
-
-  float Ar[K], Ai[K], Br[K], Bi[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) { Ar[k] = 1.f; Ai[k] = 0.f; Br[k] = 0.f; Bi[k] = 0.f; }
-#pragma unroll
-  for (int j = 0; j < L; ++j) {
-    if (t0 + j < T) {  // steps past T are the identity map (canon:497-501)
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        float v, br, bi;
-        gates(z[j][0][k], z[j][1][k], z[j][2][k], gm[k], v, br, bi);
-        const float keep = 1.f - v;
-        compose(keep * lr[k], keep * li[k], br, bi, Ar[k], Ai[k], Br[k], Bi[k]);
-      }
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    s_sum[wave][0][lane * K + k] = Ar[k];
-    s_sum[wave][1][lane * K + k] = Ai[k];
-    s_sum[wave][2][lane * K + k] = Br[k];
-    s_sum[wave][3][lane * K + k] = Bi[k];
+    s_sum[wave][0][lane * K + k] = P[k];
+    s_sum[wave][1][lane * K + k] = Br[k];
+    s_sum[wave][2][lane * K + k] = Bi[k];
   }
   __syncthreads();
   if (wave == 0 && ok) {
-    // compose the wave summaries in time order
+    float lLr[K], lLi[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) { Ar[k] = 1.f; Ai[k] = 0.f; Br[k] = 0.f; Bi[k] = 0.f; }
+    for (int k = 0; k < K; ++k) cpow(lr[k], li[k], L, lLr[k], lLi[k]);
 #pragma unroll
+    for (int k = 0; k < K; ++k) { P[k] = 1.f; Br[k] = 0.f; Bi[k] = 0.f; }
     for (int u = 0; u < W; ++u) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int x = lane * K + k;
-        compose(s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], s_sum[u][3][x], Ar[k], Ai[k],
-                Br[k], Bi[k]);
+        apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], Br[k], Bi[k]);
+        P[k] *= s_sum[u][0][x];
       }
     }
-    float* out = agg + ((int64_t)b * n_chunks + chunk) * 4 * C + c0;
-    Store<K>::run(out, Ar);
-    Store<K>::run(out + C, Ai);
-    Store<K>::run(out + 2 * C, Br);
-    Store<K>::run(out + 3 * C, Bi);
+    float* out = agg + ((int64_t)b * n_chunks + chunk) * 3 * C + c0;
+    Store<K>::run(out, P);
+    Store<K>::run(out + C, Br);
+    Store<K>::run(out + 2 * C, Bi);
   }
 }
 
-// ------------------------------------------------------------------------------------------
 // Phase 2: exclusive scan of chunk summaries per (b, c): carry[k] = state before chunk k.
 // Block = kCarryWaves waves x 64 channels; wave g owns a contiguous group of chunks.
-// carry layout [B][n_chunks][2][C]; state_in/state_out [B][2C] planar.
-// ------------------------------------------------------------------------------------------
+// carry layout [B][n_chunks][2][C]. Only chunks 0..n_chunks-2 have summaries.
 __global__ __launch_bounds__(kCarryWaves * 64) void fl_chunk_carry_kernel(
-    const float* __restrict__ agg, int C, int n_chunks, const float* __restrict__ state_in,
-    float* __restrict__ carry, float* __restrict__ state_out) {
+    const float* __restrict__ agg, int C, int n_chunks, const float* __restrict__ tr,
+    const float* __restrict__ ti, const float* __restrict__ state_in, float* __restrict__ carry) {
   __shared__ float s_grp[kCarryWaves][4][64];
   const int lane = threadIdx.x & 63;
   const int g = threadIdx.x >> 6;
   const int b = blockIdx.y;
   const int c = blockIdx.x * 64 + lane;
   const bool ok = c < C;
-  const int per = (n_chunks + kCarryWaves - 1) / kCarryWaves;
-  const int k_begin = min(g * per, n_chunks);
-  const int k_end = min(k_begin + per, n_chunks);
-  const float* ab = agg + (int64_t)b * n_chunks * 4 * C + c;
+  const int n_sum = n_chunks - 1;  // summaries that exist
+  const int per = (n_sum + kCarryWaves - 1) / kCarryWaves;
+  const int k_begin = min(g * per, n_sum);
+  const int k_end = min(k_begin + per, n_sum);
+  const float* ab = agg + (int64_t)b * n_chunks * 3 * C + c;
+  float lcr = 1.f, lci = 0.f;  // lam^kChunkT
+  if (ok) cpow(tr[c], ti[c], kChunkT, lcr, lci);
 
+  // group map as (A complex, B complex)
   float Ar = 1.f, Ai = 0.f, Br = 0.f, Bi = 0.f;
   if (ok) {
     for (int k = k_begin; k < k_end; ++k) {
-      const float* p = ab + (int64_t)k * 4 * C;
-      compose(p[0], p[C], p[2 * C], p[3 * C], Ar, Ai, Br, Bi);
+      const float* p = ab + (int64_t)k * 3 * C;
+      const float P = p[0];
+      const float ar = P * lcr, ai = P * lci;
+      const float nAr = ar * Ar - ai * Ai;
+      const float nAi = ar * Ai + ai * Ar;
+      const float nBr = ar * Br - ai * Bi + p[C];
+      const float nBi = ar * Bi + ai * Br + p[2 * C];
+      Ar = nAr; Ai = nAi; Br = nBr; Bi = nBi;
     }
   }
   s_grp[g][0][lane] = Ar;
@@ -265,136 +461,436 @@ __global__ __launch_bounds__(kCarryWaves * 64) void fl_chunk_carry_kernel(
   for (int k = k_begin; k < k_end; ++k) {
     cb[(int64_t)k * 2 * C] = sr;
     cb[(int64_t)k * 2 * C + C] = si;
-    const float* p = ab + (int64_t)k * 4 * C;
-    const float ar = p[0], ai = p[C];
-    const float nr = ar * sr - ai * si + p[2 * C];
-    const float ni = ar * si + ai * sr + p[3 * C];
-    sr = nr; si = ni;
+    const float* p = ab + (int64_t)k * 3 * C;
+    apply_map(lcr, lci, p[0], p[C], p[2 * C], sr, si);
   }
-  if (g == kCarryWaves - 1 && state_out != nullptr) {
-    state_out[(int64_t)b * 2 * C + c] = sr;
-    state_out[(int64_t)b * 2 * C + C + c] = si;
+  if (g == kCarryWaves - 1) {  // the state entering the last chunk
+    cb[(int64_t)n_sum * 2 * C] = sr;
+    cb[(int64_t)n_sum * 2 * C + C] = si;
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Phase 3: re-run each chunk from its carry-in and write
-// read[b,t,:] = [Re s | Im s | Re disp | Im disp]  (canon:583-621)
-// ------------------------------------------------------------------------------------------
+// Phase 3: re-run each chunk from its carry-in and write read (and state_out).
 template <typename RawT, int K, int L, int W>
 __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     const float* __restrict__ tr, const float* __restrict__ ti, const float* __restrict__ gamma,
-    const float* __restrict__ carry, float* __restrict__ read) {
+    const float* __restrict__ carry, float* __restrict__ read, float* __restrict__ state_out) {
   static_assert(W * L == kChunkT, "chunk length mismatch");
   constexpr int CT = 64 * K;
-  __shared__ float s_sum[W][4][CT];
+  __shared__ float s_sum[W][3][CT];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = uniform(threadIdx.x >> 6);
   const int chunk = blockIdx.x;
   const int b = blockIdx.z;
   const int c0 = blockIdx.y * CT + lane * K;
   const bool ok = c0 < C;
 
   float lr[K], li[K], gm[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) {
-    lr[k] = ok ? tr[c0 + k] : 0.f;
-    li[k] = ok ? ti[c0 + k] : 0.f;
-    gm[k] = ok ? gamma[c0 + k] : 0.f;
-  }
-
-  const int t0 = chunk * kChunkT + wave * L;
-  const RawT* base = raw + (int64_t)b * sb + c0;
-  // raw -> (v, b) per step, kept in registers between the summary and the materialisation
-  float gv[L][K], gbr[L][K], gbi[L][K];
-  {
-    float z[L][3][K];
-#pragma unroll
-    for (int j = 0; j < L; ++j) {
-      const int t = t0 + j;
-      if (ok && t < T) {
-        const RawT* p = base + (int64_t)t * st;
-        Load<RawT, K>::run(p, z[j][0]);
-        Load<RawT, K>::run(p + C, z[j][1]);
-        Load<RawT, K>::run(p + 2 * C, z[j][2]);
-      } else {
-#pragma unroll
-        for (int k = 0; k < K; ++k) z[j][0][k] = z[j][1][k] = z[j][2][k] = 0.f;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < L; ++j) {
-#pragma unroll
-      for (int k = 0; k < K; ++k) gates(z[j][0][k], z[j][1][k], z[j][2][k], gm[k], gv[j][k], gbr[j][k], gbi[j][k]);
-    }
-  }
-
+  load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
+  const int t_begin = chunk * kChunkT;
+  const TileIo io = tile_io<RawT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  WaveTile<RawT, K, L> tile;
+  tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
+  const int n = min(max(T - (t_begin + wave * L), 0), L);  // valid steps of this wave
   if (W > 1) {
     if (wave < W - 1) {
-      float Ar[K], Ai[K], Br[K], Bi[K];
-#pragma unroll
-      for (int k = 0; k < K; ++k) { Ar[k] = 1.f; Ai[k] = 0.f; Br[k] = 0.f; Bi[k] = 0.f; }
-#pragma unroll
-      for (int j = 0; j < L; ++j) {
-        if (t0 + j < T) {
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const float keep = 1.f - gv[j][k];
-            compose(keep * lr[k], keep * li[k], gbr[j][k], gbi[j][k], Ar[k], Ai[k], Br[k], Bi[k]);
-          }
-        }
-      }
+      // read only by later waves, which have valid steps only if this wave is full
+      float P[K], Br[K], Bi[K];
+      tile.summary(lr, li, P, Br, Bi);
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        s_sum[wave][0][lane * K + k] = Ar[k];
-        s_sum[wave][1][lane * K + k] = Ai[k];
-        s_sum[wave][2][lane * K + k] = Br[k];
-        s_sum[wave][3][lane * K + k] = Bi[k];
+        s_sum[wave][0][lane * K + k] = P[k];
+        s_sum[wave][1][lane * K + k] = Br[k];
+        s_sum[wave][2][lane * K + k] = Bi[k];
       }
     }
     __syncthreads();
   }
-  if (!ok) return;
-
+  if (!ok || n == 0) return;
   float sr[K], si[K];
   {
     const float* cp = carry + ((int64_t)b * n_chunks + chunk) * 2 * C + c0;
     Load<float, K>::run(cp, sr);
     Load<float, K>::run(cp + C, si);
   }
-  for (int u = 0; u < wave; ++u) {
+  if (wave > 0) {
+    float lLr[K], lLi[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) cpow(lr[k], li[k], L, lLr[k], lLi[k]);
+    for (int u = 0; u < wave; ++u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int x = lane * K + k;
+        apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr[k], si[k]);
+      }
+    }
+  }
+  tile.materialize(io.read, io.vo_read, wave * L * io.read_row, io.read_row, io.read_plane, n, lr,
+                   li, sr, si);
+  if (state_out != nullptr && t_begin + wave * L + n == T) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
-      const int x = lane * K + k;
-      const float ar = s_sum[u][0][x], ai = s_sum[u][1][x];
-      const float nr = ar * sr[k] - ai * si[k] + s_sum[u][2][x];
-      const float ni = ar * si[k] + ai * sr[k] + s_sum[u][3][x];
-      sr[k] = nr; si[k] = ni;
+      state_out[(int64_t)b * 2 * C + c0 + k] = sr[k];
+      state_out[(int64_t)b * 2 * C + C + c0 + k] = si[k];
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Single-pass path (FL_ALGO_LOOKBACK): one launch, raw read once, read written once.
+//
+// Tiles = (chain = (b, channel tile), chunk of W*L steps). Each block takes the next ticket
+// from a counter (so a block only ever waits on tiles whose tickets were taken earlier, by
+// blocks that are already resident: no deadlock); ticket -> tile is chunk-major. A tile
+//   1. loads its raw tile into registers and forms the gates;
+//   2. composes its summary (P, B) and publishes it (status AGG);
+//   3. looks back over its chain: the summaries of earlier tiles are composed until a tile
+//      with a published inclusive state (status INCL) is found, which gives the carry-in; all
+//      W waves fetch and compose predecessor summaries in parallel, up to kLookbackBatch each
+//      per round;
+//   4. publishes its inclusive state (status INCL) and materialises.
+// Every published value is a 64-bit word (value | tag), tag = epoch<<2 | kind, written and
+// read with relaxed agent-scope atomics (device-coherent across XCD L2s). A reader checks
+// each word's own tag, so no fences are needed, and the epoch (bumped by the last block of
+// every launch) makes words of earlier launches stale without clearing the workspace.
+// Waits sleep between polls and give up after kSpinLimit polls (error flag set), so every
+// wave terminates.
+// ------------------------------------------------------------------------------------------
+struct LookbackHeader {
+  unsigned long long ticket;  // bits 63..32: launch epoch, bits 31..0: next ticket
+  unsigned int done;          // tiles finished in this launch
+  unsigned int error;         // bit 0: a wait hit kSpinLimit; bit 1: ticket out of range
+};
+
+constexpr uint32_t kTagAgg = 1u;
+constexpr uint32_t kTagIncl = 2u;
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr size_t kHeaderBytes = 256;
+constexpr int kLookbackBatch = 4;  // predecessor summaries fetched per wave per round
+// data planes of a tile: P, Br, Bi (summary), Sr, Si (inclusive state)
+constexpr int kPlanes = 5;
+
+__device__ __forceinline__ void put_word(uint64_t* p, float v, uint32_t tag) {
+  const uint64_t w = ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(v);
+  __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t get_word(uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t word_tag(uint64_t w) { return (uint32_t)(w >> 32); }
+__device__ __forceinline__ float word_value(uint64_t w) { return __uint_as_float((uint32_t)w); }
+
+// Wait until every word w[i] (loaded from p[i*stride]) carries `tag`; false if the wait gave up.
+template <int N>
+__device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t tag, uint64_t* w,
+                                             uint32_t& spins) {
+  while (true) {
+    bool ready = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) ready = ready && word_tag(w[i]) == tag;
+    if (ready) return true;
+    if (++spins > kSpinLimit) return false;
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int i = 0; i < N; ++i)
+      if (word_tag(w[i]) != tag) w[i] = get_word(p + (int64_t)i * stride);
+  }
+}
+
+template <typename RawT, int K, int L, int W>
+__global__ __launch_bounds__(W * 64) void fl_scan_lookback_kernel(
+    const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
+    int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
+    const float* __restrict__ gamma, const float* __restrict__ state_in,
+    float* __restrict__ state_out, float* __restrict__ read, LookbackHeader* hdr,
+    uint32_t* status, uint64_t* data, uint32_t n_tiles) {
+  constexpr int CT = 64 * K;
+  constexpr int TC = W * L;
+  constexpr int kMaxRound = W * kLookbackBatch < 64 ? W * kLookbackBatch : 64;
+  __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
+  __shared__ float s_part[W][4][CT];  // look-back partial maps (Ar, Ai, Br, Bi)
+  __shared__ float s_carry[2][CT];
+  __shared__ int s_meta[4];           // j, n, kind, done
+  __shared__ uint32_t s_tk[2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  if (threadIdx.x == 0) {
+    const unsigned long long tk = atomicAdd(&hdr->ticket, 1ull);
+    s_tk[0] = (uint32_t)tk;
+    s_tk[1] = (uint32_t)(tk >> 32);
+  }
+  __syncthreads();
+  const uint32_t ticket = s_tk[0];
+  const uint32_t epoch = s_tk[1];
+  if (ticket >= n_tiles) {  // counter not re-armed by an interrupted launch: refuse, terminate
+    if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
+    return;
+  }
+  const uint32_t n_chains = n_tiles / (uint32_t)n_chunks;
+  const int chunk = (int)(ticket / n_chains);
+  const int chain = (int)(ticket - (uint32_t)chunk * n_chains);
+  const int b = chain / n_ctiles;
+  const int ctile = chain - b * n_ctiles;
+  const int c0 = ctile * CT + lane * K;
+  const bool ok = c0 < C;
+  const uint32_t tag_agg = ((epoch & 0x3fffffffu) << 2) | kTagAgg;
+  const uint32_t tag_incl = ((epoch & 0x3fffffffu) << 2) | kTagIncl;
+  const int t_begin = chunk * TC;
+  const bool last_chunk = chunk == n_chunks - 1;
+
+  float lr[K], li[K], gm[K];
+  load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
+  const TileIo io = tile_io<RawT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  WaveTile<RawT, K, L> tile;
+  tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
+  const int n_valid = min(max(T - (t_begin + wave * L), 0), L);
+  {
+    // full tiles are the only ones whose summary is consumed
+    float P[K], Br[K], Bi[K];
+    tile.summary(lr, li, P, Br, Bi);
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      s_sum[wave][0][lane * K + k] = P[k];
+      s_sum[wave][1][lane * K + k] = Br[k];
+      s_sum[wave][2][lane * K + k] = Bi[k];
+    }
+  }
+  float lLr[K], lLi[K], lTr[K], lTi[K];  // lam^L, lam^TC
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    cpow(lr[k], li[k], L, lLr[k], lLi[k]);
+    cpow(lLr[k], lLi[k], W, lTr[k], lTi[k]);
+  }
+  __syncthreads();
+
+  const uint32_t tile_id = (uint32_t)chain * (uint32_t)n_chunks + (uint32_t)chunk;
+  uint32_t* st_chain = status + (size_t)chain * n_chunks;
+  uint64_t* dt = data + (size_t)tile_id * kPlanes * CT + lane * K;
+  float TP[K], TBr[K], TBi[K];  // tile summary (wave 0)
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) { TP[k] = 1.f; TBr[k] = 0.f; TBi[k] = 0.f; }
+    for (int u = 0; u < W; ++u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int x = lane * K + k;
+        apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], TBr[k], TBi[k]);
+        TP[k] *= s_sum[u][0][x];
+      }
+    }
+    if (chunk > 0 && !last_chunk) {
+      if (ok) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          put_word(dt + 0 * CT + k, TP[k], tag_agg);
+          put_word(dt + 1 * CT + k, TBr[k], tag_agg);
+          put_word(dt + 2 * CT + k, TBi[k], tag_agg);
+        }
+      }
+      if (lane == 0)
+        __hip_atomic_store(st_chain + chunk, tag_agg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 
-  float* out = read + ((int64_t)b * T + t0) * 4 * C + c0;
+  // carry-in of the tile (wave 0's registers)
+  float cr[K], ci[K];
 #pragma unroll
-  for (int j = 0; j < L; ++j) {
-    if (t0 + j < T) {
-      float dr[K], di[K];
+  for (int k = 0; k < K; ++k) {
+    cr[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
+    ci[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
+  }
+  if (chunk > 0) {
+    // acc (wave 0): map from the end of the farthest consumed predecessor to the tile start
+    float aAr[K], aAi[K], aBr[K], aBi[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) { aAr[k] = 1.f; aAi[k] = 0.f; aBr[k] = 0.f; aBi[k] = 0.f; }
+    uint32_t spins = 0;
+    bool failed = false;
+    int j = chunk - 1;  // nearest predecessor not yet consumed
+    while (true) {
+      if (wave == 0) {
+        const int p = j - lane;
+        uint32_t s = 0;
+        if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
+        const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
+        int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
+        int n;
+        if (i0 >= kMaxRound) {
+          n = kMaxRound;
+          kind = 1;
+        } else {
+          n = i0;
+          const uint32_t s_at = __shfl(s, i0);
+          const int p_at = __shfl(p, i0);
+          kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
+        }
+        if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
+      }
+      __syncthreads();
+      const int jj = s_meta[0], n = s_meta[1], kind = s_meta[2];
+      // this wave composes predecessors jj - i for i in [lo, hi), nearest first
+      const int m = (n + W - 1) / W;
+      const int lo = min(wave * m, n), hi = min(lo + m, n);
+      {
+        float pAr[K], pAi[K], pBr[K], pBi[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) { pAr[k] = 1.f; pAi[k] = 0.f; pBr[k] = 0.f; pBi[k] = 0.f; }
+        if (ok && hi > lo) {
+          uint64_t w[kLookbackBatch][3][K];
+#pragma unroll
+          for (int q = 0; q < kLookbackBatch; ++q) {
+            if (lo + q < hi) {
+              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - lo - q)) * kPlanes * CT + lane * K;
+#pragma unroll
+              for (int k = 0; k < K; ++k) {
+                w[q][0][k] = get_word(dp + k);
+                w[q][1][k] = get_word(dp + CT + k);
+                w[q][2][k] = get_word(dp + 2 * CT + k);
+              }
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < kLookbackBatch; ++q) {
+            if (lo + q < hi && !failed) {
+              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - lo - q)) * kPlanes * CT + lane * K;
+#pragma unroll
+              for (int k = 0; k < K; ++k) {
+                uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
+                if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins)) { failed = true; break; }
+                // partial <- partial o M(pred), with A(pred) = lam^TC * P
+                const float P = word_value(ww[0]);
+                const float ar = P * lTr[k], ai = P * lTi[k];
+                const float qBr = word_value(ww[1]), qBi = word_value(ww[2]);
+                const float nBr = pAr[k] * qBr - pAi[k] * qBi + pBr[k];
+                const float nBi = pAr[k] * qBi + pAi[k] * qBr + pBi[k];
+                const float nAr = pAr[k] * ar - pAi[k] * ai;
+                const float nAi = pAr[k] * ai + pAi[k] * ar;
+                pAr[k] = nAr; pAi[k] = nAi; pBr[k] = nBr; pBi[k] = nBi;
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          s_part[wave][0][lane * K + k] = pAr[k];
+          s_part[wave][1][lane * K + k] = pAi[k];
+          s_part[wave][2][lane * K + k] = pBr[k];
+          s_part[wave][3][lane * K + k] = pBi[k];
+        }
+      }
+      if (kind == 2 && wave == W - 1 && ok) {  // inclusive state of predecessor jj - n
+        uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - n)) * kPlanes * CT + lane * K;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
+          if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
+          s_carry[0][lane * K + k] = word_value(ww[0]);
+          s_carry[1][lane * K + k] = word_value(ww[1]);
+        }
+      }
+      if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
+      __syncthreads();
+      if (wave == 0) {
+        // acc <- acc o part_0 o part_1 o ...  (part_u covers nearer predecessors than part_u+1)
+        for (int u = 0; u < W; ++u) {
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int x = lane * K + k;
+            const float qAr = s_part[u][0][x], qAi = s_part[u][1][x];
+            const float qBr = s_part[u][2][x], qBi = s_part[u][3][x];
+            const float nBr = aAr[k] * qBr - aAi[k] * qBi + aBr[k];
+            const float nBi = aAr[k] * qBi + aAi[k] * qBr + aBi[k];
+            const float nAr = aAr[k] * qAr - aAi[k] * qAi;
+            const float nAi = aAr[k] * qAi + aAi[k] * qAr;
+            aAr[k] = nAr; aAi[k] = nAi; aBr[k] = nBr; aBi[k] = nBi;
+          }
+        }
+        int done = 0;
+        if (kind == 2) {
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            const int x = lane * K + k;
+            const float sr = s_carry[0][x], si = s_carry[1][x];
+            cr[k] = aAr[k] * sr - aAi[k] * si + aBr[k];
+            ci[k] = aAr[k] * si + aAi[k] * sr + aBi[k];
+          }
+          done = 1;
+        } else if (kind == 0) {
+          if (++spins > kSpinLimit) {
+            failed = true;
+            if (lane == 0) atomicOr(&hdr->error, 1u);
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+        if (__ballot(failed) != 0ull) done = 1;  // give up: the carry stays state_in / 0
+        if (lane == 0) s_meta[3] = done;
+      }
+      __syncthreads();
+      const int finished = s_meta[3];
+      if (finished) break;
+      j = jj - n;
+      __syncthreads();  // s_meta is rewritten by the next round
+    }
+  }
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      s_carry[0][lane * K + k] = cr[k];
+      s_carry[1][lane * K + k] = ci[k];
+    }
+    // publish the inclusive state (every tile but the last of its chain has a successor)
+    if (!last_chunk) {
+      if (ok) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          float sr = cr[k], si = ci[k];
+          apply_map(lTr[k], lTi[k], TP[k], TBr[k], TBi[k], sr, si);
+          put_word(dt + 3 * CT + k, sr, tag_incl);
+          put_word(dt + 4 * CT + k, si, tag_incl);
+        }
+      }
+      if (lane == 0)
+        __hip_atomic_store(st_chain + chunk, tag_incl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+
+  if (ok && n_valid > 0) {
+    float sr[K], si[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      sr[k] = s_carry[0][lane * K + k];
+      si[k] = s_carry[1][lane * K + k];
+    }
+    for (int u = 0; u < wave; ++u) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        // s + disp = lam*s_prev + b, disp = v*lam*s_prev
-        const float mr = lr[k] * sr[k] - li[k] * si[k];
-        const float mi = lr[k] * si[k] + li[k] * sr[k];
-        dr[k] = gv[j][k] * mr;
-        di[k] = gv[j][k] * mi;
-        sr[k] = mr - dr[k] + gbr[j][k];
-        si[k] = mi - di[k] + gbi[j][k];
+        const int x = lane * K + k;
+        apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr[k], si[k]);
       }
-      float* o = out + (int64_t)j * 4 * C;
-      Store<K>::run(o, sr);
-      Store<K>::run(o + C, si);
-      Store<K>::run(o + 2 * C, dr);
-      Store<K>::run(o + 3 * C, di);
+    }
+    tile.materialize(io.read, io.vo_read, wave * L * io.read_row, io.read_row, io.read_plane,
+                     n_valid, lr, li, sr, si);
+    if (state_out != nullptr && t_begin + wave * L + n_valid == T) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        state_out[(int64_t)b * 2 * C + c0 + k] = sr[k];
+        state_out[(int64_t)b * 2 * C + C + c0 + k] = si[k];
+      }
+    }
+  }
+
+  // the last block of the launch re-arms the counter for the next launch (next epoch)
+  if (threadIdx.x == 0) {
+    const unsigned int d = atomicAdd(&hdr->done, 1u);
+    if (d == n_tiles - 1) {
+      __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&hdr->ticket, (unsigned long long)(epoch + 1u) << 32, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -434,8 +930,8 @@ __global__ __launch_bounds__(256) void fl_decode_step_kernel(
     const float mi = lr[k] * si[k] + li[k] * sr[k];
     dr[k] = v * mr;
     di[k] = v * mi;
-    sr[k] = mr - dr[k] + br;
-    si[k] = mi - di[k] + bi;
+    sr[k] = (mr - dr[k]) + br;
+    si[k] = (mi - di[k]) + bi;
   }
   Store<K>::run(s, sr);
   Store<K>::run(s + C, si);
@@ -469,6 +965,57 @@ int pick_k(int raw_dtype, const void* raw, int64_t C, int64_t sb, int64_t st, co
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? FL_OK : FL_ERR_HIP_BASE + (int)e; }
 
+// Look-back tilings: (K channels per lane, L steps per wave, W waves per block).
+// Variant 0 is the default; the others are selectable for tuning (algo >> 8).
+struct LookbackTiling {
+  int k, l, w;
+};
+constexpr LookbackTiling kLookbackTilings[] = {
+    {1, 16, 8}, {1, 8, 8}, {2, 8, 8}, {1, 16, 4}, {1, 32, 4}, {2, 16, 4}, {1, 8, 4}, {2, 8, 4},
+};
+constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
+
+// Workspace layout, fixed for a shape whatever the algorithm or tiling:
+//   [header 256 B][status: max tiles x u32][data: max tiles x 5 x CT x u64][chunked3 floats]
+// Status words and data words are only ever written as tagged words (by any tiling), and the
+// three-phase buffers have their own region, so a word left by another call can never carry
+// the current launch's tag.
+struct WorkspaceLayout {
+  size_t status_off, data_off, chunked3_off, bytes;
+};
+
+struct LookbackGeom {
+  int n_chunks, n_ctiles;
+  uint32_t n_tiles;
+};
+
+LookbackGeom lookback_geom(int64_t B, int64_t T, int64_t C, int CT, int TC) {
+  LookbackGeom g;
+  g.n_chunks = (int)cdiv(T, TC);
+  g.n_ctiles = (int)cdiv(C, CT);
+  g.n_tiles = (uint32_t)(B * g.n_ctiles * (int64_t)g.n_chunks);
+  return g;
+}
+
+WorkspaceLayout workspace_layout(int64_t B, int64_t T, int64_t C) {
+  size_t max_tiles = 0, max_data = 0;
+  for (int v = 0; v < kNumLookbackTilings; ++v) {
+    const LookbackTiling tl = kLookbackTilings[v];
+    for (int k = tl.k; k >= 1; k /= 2) {  // narrowed variants have smaller CT
+      const LookbackGeom g = lookback_geom(B, T, C, 64 * k, tl.l * tl.w);
+      const size_t data = (size_t)g.n_tiles * kPlanes * (64 * k) * sizeof(uint64_t);
+      if (g.n_tiles > max_tiles) max_tiles = g.n_tiles;
+      if (data > max_data) max_data = data;
+    }
+  }
+  WorkspaceLayout w;
+  w.status_off = kHeaderBytes;
+  w.data_off = w.status_off + (size_t)cdiv((int64_t)max_tiles * 4, 256) * 256;
+  w.chunked3_off = w.data_off + (size_t)cdiv((int64_t)max_data, 256) * 256;
+  w.bytes = w.chunked3_off + (size_t)(B * cdiv(T, kChunkT) * C) * 5 * sizeof(float);
+  return w;
+}
+
 template <typename RawT, int K>
 int launch_chunked3(const RawT* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
@@ -481,12 +1028,12 @@ int launch_chunked3(const RawT* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
   const dim3 cgrid((unsigned)cdiv(C, 64), (unsigned)B);
-  fl_chunk_carry_kernel<<<cgrid, kCarryWaves * 64, 0, stream>>>(agg, (int)C, n_chunks, state_in,
-                                                                 carry, state_out);
+  fl_chunk_carry_kernel<<<cgrid, kCarryWaves * 64, 0, stream>>>(agg, (int)C, n_chunks, tr, ti,
+                                                                 state_in, carry);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
   fl_chunk_materialize_kernel<RawT, K, 8, 8><<<grid, 8 * 64, 0, stream>>>(
-      raw, sb, st, (int)T, (int)C, n_chunks, tr, ti, gamma, carry, read);
+      raw, sb, st, (int)T, (int)C, n_chunks, tr, ti, gamma, carry, read, state_out);
   return hip_status(hipGetLastError());
 }
 
@@ -507,6 +1054,39 @@ int dispatch_chunked3(int k, const void* raw, int64_t B, int64_t T, int64_t C, i
       return launch_chunked3<RawT, 1>(r, B, T, C, sb, st, tr, ti, gamma, state_in, state_out,
                                       read, agg, carry, stream);
   }
+}
+
+template <typename RawT, int K, int L, int W>
+int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
+                    const float* tr, const float* ti, const float* gamma, const float* state_in,
+                    float* state_out, float* read, void* workspace, hipStream_t stream) {
+  constexpr int CT = 64 * K;
+  const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
+  const WorkspaceLayout lay = workspace_layout(B, T, C);
+  char* ws = static_cast<char*>(workspace);
+  fl_scan_lookback_kernel<RawT, K, L, W><<<g.n_tiles, W * 64, 0, stream>>>(
+      static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
+      gamma, state_in, state_out, read, reinterpret_cast<LookbackHeader*>(ws),
+      reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
+      g.n_tiles);
+  return hip_status(hipGetLastError());
+}
+
+template <typename RawT>
+int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T, int64_t C,
+                      int64_t sb, int64_t st, const float* tr, const float* ti, const float* gamma,
+                      const float* state_in, float* state_out, float* read, void* ws,
+                      hipStream_t s) {
+  const LookbackTiling tl = kLookbackTilings[variant];
+  const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
+#define FL_LB(KK, LL, WW)                                                                   \
+  if (kk == KK && tl.l == LL && tl.w == WW)                                                  \
+    return launch_lookback<RawT, KK, LL, WW>(raw, B, T, C, sb, st, tr, ti, gamma, state_in, \
+                                             state_out, read, ws, s);
+  FL_LB(1, 16, 8) FL_LB(1, 8, 8) FL_LB(2, 8, 8) FL_LB(1, 16, 4) FL_LB(1, 32, 4) FL_LB(2, 16, 4)
+  FL_LB(1, 8, 4) FL_LB(2, 8, 4)
+#undef FL_LB
+  return FL_ERR_INVALID_ARGUMENT;
 }
 
 template <typename RawT>
@@ -533,23 +1113,25 @@ int dispatch_decode(int k, const void* raw_t, int64_t B, int64_t C, int64_t sb, 
   return hip_status(hipGetLastError());
 }
 
-// shape limits of the launch geometry: grid.y = C/(64K) and grid.z = B stay <= 65535,
-// int32 element counts per row
+// Shape limits: grid.y = C/(64K) and grid.z = B stay <= 65535; the buffer descriptors of a
+// tile (from its first row to the end of its batch row) and every byte offset inside them
+// stay below 2^31; the look-back tile count stays below 2^31.
 constexpr int64_t kMaxB = 65535;
-constexpr int64_t kMaxC = (int64_t)1 << 20;
+constexpr int64_t kMaxC = (int64_t)1 << 16;
 constexpr int64_t kMaxT = (int64_t)1 << 30;
+constexpr int64_t kMaxBufferBytes = ((int64_t)1 << 31) - 1;
+constexpr int64_t kMaxRowBytes = (int64_t)1 << 22;  // 512 rows of a tile stay below 2^31 bytes
 
 size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
   if (B <= 0 || T <= 0 || C <= 0) return 0;
-  const int64_t n_chunks = cdiv(T, kChunkT);
-  return (size_t)(B * n_chunks * C) * 6 * sizeof(float) + 256;
+  return workspace_layout(B, T, C).bytes;
 }
 
 }  // namespace
 
 extern "C" {
 
-const char* fl_version(void) { return "fields_amd 0.1 gfx950"; }
+const char* fl_version(void) { return "fields_amd 0.3 gfx950"; }
 
 size_t fl_scan_workspace_bytes(int64_t B, int64_t T, int64_t C) { return workspace_bytes(B, T, C); }
 
@@ -560,31 +1142,48 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
                        size_t workspace_bytes_given, int algo, void* stream) {
   if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   if (read_dtype != FL_DTYPE_F32) return FL_ERR_DTYPE;
-  if (algo != FL_ALGO_AUTO && algo != FL_ALGO_CHUNKED3) return FL_ERR_INVALID_ARGUMENT;
+  const int base_algo = algo & 0xff;
+  const int variant = algo >> 8;
+  if (base_algo != FL_ALGO_AUTO && base_algo != FL_ALGO_CHUNKED3 && base_algo != FL_ALGO_LOOKBACK)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (variant < 0 || variant >= kNumLookbackTilings) return FL_ERR_INVALID_ARGUMENT;
   if (B <= 0 || T <= 0 || C <= 0 || B > kMaxB || C > kMaxC || T > kMaxT)
     return FL_ERR_INVALID_ARGUMENT;
   if (raw_stride_t < 3 * C || raw_stride_b < 0) return FL_ERR_INVALID_ARGUMENT;
   if (B > 1 && raw_stride_b < (T - 1) * raw_stride_t + 3 * C) return FL_ERR_INVALID_ARGUMENT;
+  const int64_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  // per batch row, raw and read rows are addressed through 32-bit buffer offsets
+  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * 4 > kMaxBufferBytes)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (raw_stride_t * esz > kMaxRowBytes || 4 * C * 4 > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
+  if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!raw || !tr || !ti || !gamma || !read) return FL_ERR_INVALID_ARGUMENT;
   const size_t need = workspace_bytes(B, T, C);
   if (!workspace || workspace_bytes_given < need) return FL_ERR_WORKSPACE;
-  const size_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
-  if (!aligned(raw, esz) || !aligned(read, 4) || !aligned(workspace, 16))
+  if (!aligned(raw, esz) || !aligned(read, 4) || !aligned(workspace, 256))
     return FL_ERR_INVALID_ARGUMENT;
   if ((state_in && !aligned(state_in, 4)) || (state_out && !aligned(state_out, 4)))
     return FL_ERR_INVALID_ARGUMENT;
 
   const int k = pick_k(raw_dtype, raw, C, raw_stride_b, raw_stride_t, read, nullptr, nullptr);
-  const int64_t n_chunks = cdiv(T, kChunkT);
-  float* agg = static_cast<float*>(workspace);
-  float* carry = agg + B * n_chunks * 4 * C;
   hipStream_t s = static_cast<hipStream_t>(stream);
   float* rd = static_cast<float*>(read);
+  if (base_algo == FL_ALGO_CHUNKED3) {
+    const int64_t n_chunks = cdiv(T, kChunkT);
+    float* agg = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                          workspace_layout(B, T, C).chunked3_off);
+    float* carry = agg + B * n_chunks * 3 * C;
+    if (raw_dtype == FL_DTYPE_BF16)
+      return dispatch_chunked3<bf16_bits>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti,
+                                          gamma, state_in, state_out, rd, agg, carry, s);
+    return dispatch_chunked3<float>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma,
+                                    state_in, state_out, rd, agg, carry, s);
+  }
   if (raw_dtype == FL_DTYPE_BF16)
-    return dispatch_chunked3<bf16_bits>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti,
-                                        gamma, state_in, state_out, rd, agg, carry, s);
-  return dispatch_chunked3<float>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma,
-                                  state_in, state_out, rd, agg, carry, s);
+    return dispatch_lookback<bf16_bits>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr,
+                                        ti, gamma, state_in, state_out, rd, workspace, s);
+  return dispatch_lookback<float>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti,
+                                  gamma, state_in, state_out, rd, workspace, s);
 }
 
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,

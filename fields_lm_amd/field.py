@@ -80,11 +80,11 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
             sout.copy_(sin if sin is not None else torch.zeros_like(sout))
         return (read, sout) if return_state else read
     ws_bytes = int(lib.fl_scan_workspace_bytes(batch, length, channels))
-    workspace = torch.empty(ws_bytes, device=dev, dtype=torch.uint8)
+    workspace = nat.scan_workspace(dev, ws_bytes)
     code = lib.fl_scan_forward_ex(
         nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels,
         raw.stride(0), raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
-        nat.ptr(sout), nat.ptr(read), nat.FL_DTYPE_F32, nat.ptr(workspace), ws_bytes, algo,
+        nat.ptr(sout), nat.ptr(read), nat.FL_DTYPE_F32, nat.ptr(workspace), workspace.numel(), algo,
         nat.stream_handle(dev))
     nat.check(code, "fl_scan_forward")
     return (read, sout) if return_state else read
@@ -299,6 +299,7 @@ class ScanPlan:
     def __init__(self, raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
                  gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
                  algo: int = nat.FL_ALGO_AUTO):
+        self.algo = algo
         self.lib = nat.load()
         batch, length, channels = _check_scan_inputs(raw, transition_r)
         if raw.stride(2) != 1:
@@ -313,7 +314,7 @@ class ScanPlan:
         self.read = torch.empty((batch, length, 4 * channels), device=dev, dtype=torch.float32)
         self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
         self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
-        self.workspace = torch.empty(self.ws_bytes, device=dev, dtype=torch.uint8)
+        self.workspace = torch.zeros(self.ws_bytes, device=dev, dtype=torch.uint8)  # zero-filled once
         self.args = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
                      raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
                      nat.ptr(self.state_out), nat.ptr(self.read), nat.FL_DTYPE_F32,

@@ -35,9 +35,11 @@ extern "C" {
 #define FL_DTYPE_F32 0
 #define FL_DTYPE_BF16 1
 
-/* algorithm selector for fl_scan_forward_ex */
+/* algorithm selector for fl_scan_forward_ex (low 8 bits); bits 8.. select a tiling variant of
+ * FL_ALGO_LOOKBACK for tuning (0 = default) */
 #define FL_ALGO_AUTO 0
 #define FL_ALGO_CHUNKED3 1 /* chunk summary -> chunk carry -> chunk materialise (three launches) */
+#define FL_ALGO_LOOKBACK 2 /* single launch, decoupled look-back across chunks (default) */
 
 #define FL_OK 0
 #define FL_ERR_INVALID_ARGUMENT 1 /* shape / stride / pointer check failed (Python: ValueError) */
@@ -62,7 +64,10 @@ extern "C" {
  *   state_in   [B, 2C] fp32 planar, or NULL for the zero state
  *   state_out  [B, 2C] fp32 planar, or NULL; receives s[T-1]
  *   read       [B, T, 4C] contiguous, read_dtype (FL_DTYPE_F32 only for now)
- *   workspace  device scratch of at least fl_scan_workspace_bytes(B, T, C) bytes
+ *   workspace  device scratch of at least fl_scan_workspace_bytes(B, T, C) bytes, 256-byte
+ *              aligned, ZERO-FILLED before its first use and then reused as is: its first 256
+ *              bytes hold a launch counter that every call leaves ready for the next one. Calls
+ *              on one workspace must be stream-ordered (one workspace per stream).
  */
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,

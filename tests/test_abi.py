@@ -52,15 +52,20 @@ def test_header_constants_match_binding():
 
 def test_version_and_workspace_size(lib):
     assert lib.fl_version().decode().startswith("fields_amd")
-    n_chunks = (2048 + 63) // 64
-    assert lib.fl_scan_workspace_bytes(8, 2048, 512) == 8 * n_chunks * 512 * 24 + 256
+    # header + look-back status/data regions + the three-phase buffers (20 B per channel-chunk)
+    for B, T, C in [(8, 2048, 512), (1, 65536, 512), (2, 37, 5)]:
+        n = lib.fl_scan_workspace_bytes(B, T, C)
+        chunked3 = B * ((T + 63) // 64) * C * 20
+        lookback = B * ((T + 31) // 32) * ((C + 63) // 64) * 64 * 40  # smallest tiles
+        assert n >= 256 + chunked3 + lookback, (B, T, C, n)
+        assert n % 4 == 0
     assert lib.fl_scan_workspace_bytes(0, 2048, 512) == 0
-    assert lib.fl_scan_workspace_bytes(1, 65536, 512) == 1024 * 512 * 24 + 256
+    assert lib.fl_scan_workspace_bytes(8, 4096, 512) > lib.fl_scan_workspace_bytes(8, 2048, 512)
 
 
 def _scan(lib, **kw):
-    a = dict(raw=16, raw_dtype=0, B=1, T=4, C=8, sb=4 * 24, st=24, tr=16, ti=16, gamma=16,
-             state_in=None, state_out=None, read=16, read_dtype=0, ws=16, ws_bytes=1 << 20,
+    a = dict(raw=256, raw_dtype=0, B=1, T=4, C=8, sb=4 * 24, st=24, tr=256, ti=256, gamma=256,
+             state_in=None, state_out=None, read=256, read_dtype=0, ws=256, ws_bytes=1 << 20,
              algo=0, stream=None)
     a.update(kw)
     return lib.fl_scan_forward_ex(a["raw"], a["raw_dtype"], a["B"], a["T"], a["C"], a["sb"], a["st"],
@@ -79,9 +84,11 @@ def test_argument_validation_returns_before_launch(lib):
     assert _scan(lib, raw=None) == nat.FL_ERR_INVALID_ARGUMENT
     assert _scan(lib, read=None) == nat.FL_ERR_INVALID_ARGUMENT
     assert _scan(lib, algo=9) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan(lib, algo=nat.FL_ALGO_LOOKBACK | (99 << 8)) == nat.FL_ERR_INVALID_ARGUMENT
     assert _scan(lib, ws=None) == nat.FL_ERR_WORKSPACE
     assert _scan(lib, ws_bytes=10) == nat.FL_ERR_WORKSPACE
-    assert _scan(lib, raw=17) == nat.FL_ERR_INVALID_ARGUMENT  # misaligned bf16/f32 pointer
+    assert _scan(lib, raw=257) == nat.FL_ERR_INVALID_ARGUMENT  # misaligned bf16/f32 pointer
+    assert _scan(lib, ws=264) == nat.FL_ERR_INVALID_ARGUMENT  # workspace not 256-byte aligned
     assert lib.fl_decode_step(16, 3, 1, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_DTYPE
     assert lib.fl_decode_step(16, 0, 0, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
     assert lib.fl_decode_step(16, 0, 1, 8, 23, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT

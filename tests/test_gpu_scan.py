@@ -45,22 +45,106 @@ SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130
           (4, 257, 512), (2, 1000, 1024)]
 
 
+ALGOS = {"lookback": 2, "chunked3": 1}
+
+
+@pytest.mark.parametrize("algo", list(ALGOS))
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 @pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
-def test_scan_matches_oracle(dev, shape, dtype):
+def test_scan_matches_oracle(dev, shape, dtype, algo):
     from fields_lm_amd import field_scan
 
     B, T, C = shape
-    print(f"[case] scan shape={shape} dtype={dtype}", flush=True)
+    print(f"[case] scan shape={shape} dtype={dtype} algo={algo}", flush=True)
     g = torch.Generator().manual_seed(B * 1000 + T + C)
     raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
     tr, ti, gamma = _params(C, seed=C)
-    read, state = field_scan(*_to(dev, raw, tr, ti, gamma), return_state=True)
+    read, state = field_scan(*_to(dev, raw, tr, ti, gamma), return_state=True, algo=ALGOS[algo])
     torch.cuda.synchronize()
     exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma)
     assert oracle.rel_err(read.cpu(), exp_read) <= TOL
     assert oracle.rel_err(state.cpu(), exp_state) <= TOL
     assert torch.isfinite(read).all()
+
+
+@pytest.mark.parametrize("variant", range(8))
+def test_lookback_tilings(dev, variant):
+    """Every look-back tiling (algo bits 8..) on ragged shapes, fp32 and bf16, with state_in."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan
+
+    print(f"[case] lookback variant={variant}", flush=True)
+    for (B, T, C, dtype) in [(3, 1000, 512, torch.bfloat16), (2, 333, 96, torch.float32),
+                             (1, 4099, 64, torch.bfloat16), (2, 50, 7, torch.float32)]:
+        g = torch.Generator().manual_seed(variant * 100 + C)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+        sin = torch.randn(B, 2 * C, generator=g) * 0.2
+        tr, ti, gamma = _params(C, seed=C + 1)
+        read, state = field_scan(*_to(dev, raw, tr, ti, gamma), state_in=sin.to(dev), return_state=True,
+                                 algo=nat.FL_ALGO_LOOKBACK | (variant << 8))
+        exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
+        assert oracle.rel_err(read.cpu(), exp_read) <= TOL, (B, T, C)
+        assert oracle.rel_err(state.cpu(), exp_state) <= TOL, (B, T, C)
+
+
+def test_workspace_reuse_across_shapes_and_algos(dev):
+    """One workspace, calls alternating shape, dtype, algorithm and tiling: every result stays
+    exact and the look-back error word stays 0 (stale words never match a later launch)."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan
+
+    print("[case] workspace reuse", flush=True)
+    cases = []
+    for i, (B, T, C) in enumerate([(2, 700, 256), (4, 130, 512), (1, 2000, 64), (2, 700, 256)]):
+        g = torch.Generator().manual_seed(40 + i)
+        raw = torch.randn(B, T, 3 * C, generator=g) * 2
+        tr, ti, gamma = _params(C, seed=40 + i)
+        cases.append((raw, tr, ti, gamma, oracle.scan_f64(raw, tr, ti, gamma)[0]))
+    algos = [nat.FL_ALGO_LOOKBACK, nat.FL_ALGO_CHUNKED3, nat.FL_ALGO_LOOKBACK | (3 << 8),
+             nat.FL_ALGO_LOOKBACK | (1 << 8), nat.FL_ALGO_AUTO]
+    for rep in range(3):
+        for ci, (raw, tr, ti, gamma, expect) in enumerate(cases):
+            algo = algos[(rep + ci) % len(algos)]
+            dt = torch.bfloat16 if (rep + ci) % 2 else torch.float32
+            r = raw.to(dt)
+            e = expect if dt == torch.float32 else oracle.scan_f64(r.float(), tr, ti, gamma)[0]
+            read = field_scan(*_to(dev, r, tr, ti, gamma), algo=algo)
+            assert oracle.rel_err(read.cpu(), e) <= TOL, (rep, ci, algo)
+    torch.cuda.synchronize()
+    for ws in nat._workspaces.values():
+        assert nat.workspace_error(ws) == 0
+
+
+def test_scan_plan_graph_replays(dev):
+    """ScanPlan captured in a HIP graph: each replay (raw refilled between replays, eager work
+    and synchronisations in between) equals an eager scan."""
+    from fields_lm_amd import ScanPlan, field_scan
+
+    print("[case] ScanPlan graph", flush=True)
+    B, T, C = 2, 600, 128
+    tr, ti, gamma = _to(dev, *_params(C, 3))
+    raw = torch.zeros(B, T, 3 * C, device=dev, dtype=torch.bfloat16)
+    plan = ScanPlan(raw, tr, ti, gamma)
+    plan.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+    g = torch.Generator().manual_seed(3)
+    for _ in range(5):
+        src = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+        raw.copy_(src.to(dev))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager, state = field_scan(raw, tr, ti, gamma, return_state=True)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(plan.read, eager, rtol=0, atol=0)
+        torch.testing.assert_close(plan.state_out, state, rtol=0, atol=0)
+        exp_read, _ = oracle.scan_f64(src.float(), tr.cpu(), ti.cpu(), gamma.cpu())
+        assert oracle.rel_err(plan.read.cpu(), exp_read) <= TOL
+    from fields_lm_amd import _native as nat
+
+    assert nat.workspace_error(plan.workspace) == 0
 
 
 def test_scan_state_in_continuation(dev):
