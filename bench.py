@@ -33,6 +33,40 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def copy_calibration() -> int:
+    """Plain device copy of a known size (256 MiB, 10 times): the reference reading for the
+    FETCH_SIZE / WRITE_SIZE counters (profiles/*pmc*.txt give the scale factors)."""
+    import torch
+
+    n = 256 * 2**20 // 4
+    x = torch.randn(n, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(10):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 10}), flush=True)
+    return 0
+
+
+def measured_traffic(workload: str):
+    """HBM bytes per launch of the scan from the committed rocprofv3 --pmc summary, or None."""
+    path = REPO / "profiles" / f"fl_scan_lookback_kernel_{workload}_pmc.txt"
+    if not path.exists():
+        return None
+    vals = {}
+    for line in path.read_text().splitlines():
+        if "=" in line and not line.startswith("#") and not line.startswith("cmd"):
+            k, v = line.split("=", 1)
+            try:
+                vals[k.strip()] = float(v.strip())
+            except ValueError:
+                pass
+    try:
+        return (vals["fetch_kib"] * vals["fetch_factor"] + vals["write_kib"] * vals["write_factor"]) * 1024
+    except KeyError:
+        return None
+
+
 def time_plan(plan, steps: int, warmup: int):
     """Returns (wall ms per step, event ms per step). Events sit on the launch stream."""
     import torch
@@ -144,7 +178,11 @@ def main() -> int:
     ap.add_argument("--workload", default="scan_b8_t2048_d1024")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
     args = ap.parse_args()
+    if args.copy_calibration:
+        return copy_calibration()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -193,12 +231,12 @@ def main() -> int:
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "fl_scan_forward (summary + carry + materialize launches)",
+            "kernel": "fl_scan_lookback_kernel (one launch per step)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(args.workload),
             "algorithmic_bytes": alg_bytes,
             "event_us_per_launch": ev_ms * 1e3,
         },

@@ -568,7 +568,7 @@ constexpr uint32_t kTagAgg = 1u;
 constexpr uint32_t kTagIncl = 2u;
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 256;
-constexpr int kLookbackBatch = 4;  // predecessor summaries fetched per wave per round
+constexpr int kLookbackBatch = 2;  // predecessor summaries fetched per wave per round
 // data planes of a tile: P, Br, Bi (summary), Sr, Si (inclusive state)
 constexpr int kPlanes = 5;
 
@@ -599,8 +599,8 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
   }
 }
 
-template <typename RawT, int K, int L, int W>
-__global__ __launch_bounds__(W * 64) void fl_scan_lookback_kernel(
+template <typename RawT, int K, int L, int W, int OCC>
+__global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
@@ -609,6 +609,7 @@ __global__ __launch_bounds__(W * 64) void fl_scan_lookback_kernel(
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   constexpr int kMaxRound = W * kLookbackBatch < 64 ? W * kLookbackBatch : 64;
+  static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
   __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
   __shared__ float s_part[W][4][CT];  // look-back partial maps (Ar, Ai, Br, Bi)
   __shared__ float s_carry[2][CT];
@@ -965,13 +966,15 @@ int pick_k(int raw_dtype, const void* raw, int64_t C, int64_t sb, int64_t st, co
 
 inline int hip_status(hipError_t e) { return e == hipSuccess ? FL_OK : FL_ERR_HIP_BASE + (int)e; }
 
-// Look-back tilings: (K channels per lane, L steps per wave, W waves per block).
+// Look-back tilings: (K channels per lane, L steps per wave, W waves per block, OCC target
+// waves per SIMD, which caps the VGPR budget so that OCC*4/W blocks share a CU).
 // Variant 0 is the default; the others are selectable for tuning (algo >> 8).
 struct LookbackTiling {
-  int k, l, w;
+  int k, l, w, occ;
 };
 constexpr LookbackTiling kLookbackTilings[] = {
-    {1, 16, 8}, {1, 8, 8}, {2, 8, 8}, {1, 16, 4}, {1, 32, 4}, {2, 16, 4}, {1, 8, 4}, {2, 8, 4},
+    {1, 16, 8, 4}, {1, 16, 8, 2}, {1, 16, 8, 6}, {1, 32, 4, 4},
+    {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4},  {1, 16, 4, 4},
 };
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
 
@@ -1056,7 +1059,7 @@ int dispatch_chunked3(int k, const void* raw, int64_t B, int64_t T, int64_t C, i
   }
 }
 
-template <typename RawT, int K, int L, int W>
+template <typename RawT, int K, int L, int W, int OCC>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
                     float* state_out, float* read, void* workspace, hipStream_t stream) {
@@ -1064,7 +1067,7 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
   const WorkspaceLayout lay = workspace_layout(B, T, C);
   char* ws = static_cast<char*>(workspace);
-  fl_scan_lookback_kernel<RawT, K, L, W><<<g.n_tiles, W * 64, 0, stream>>>(
+  fl_scan_lookback_kernel<RawT, K, L, W, OCC><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, read, reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
@@ -1079,12 +1082,14 @@ int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T,
                       hipStream_t s) {
   const LookbackTiling tl = kLookbackTilings[variant];
   const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
-#define FL_LB(KK, LL, WW)                                                                   \
-  if (kk == KK && tl.l == LL && tl.w == WW)                                                  \
-    return launch_lookback<RawT, KK, LL, WW>(raw, B, T, C, sb, st, tr, ti, gamma, state_in, \
-                                             state_out, read, ws, s);
-  FL_LB(1, 16, 8) FL_LB(1, 8, 8) FL_LB(2, 8, 8) FL_LB(1, 16, 4) FL_LB(1, 32, 4) FL_LB(2, 16, 4)
-  FL_LB(1, 8, 4) FL_LB(2, 8, 4)
+#define FL_LB(KK, LL, WW, OO)                                                                   \
+  if (kk == KK && tl.l == LL && tl.w == WW && tl.occ == OO)                                      \
+    return launch_lookback<RawT, KK, LL, WW, OO>(raw, B, T, C, sb, st, tr, ti, gamma, state_in, \
+                                                 state_out, read, ws, s);
+  FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 16, 8, 6) FL_LB(1, 32, 4, 4) FL_LB(1, 32, 4, 3)
+  FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4) FL_LB(1, 16, 4, 4)
+  // narrowed K (alignment): same L, W, OCC
+  FL_LB(1, 16, 4, 3) FL_LB(1, 8, 8, 4)
 #undef FL_LB
   return FL_ERR_INVALID_ARGUMENT;
 }

@@ -56,7 +56,7 @@ def test_version_and_workspace_size(lib):
     for B, T, C in [(8, 2048, 512), (1, 65536, 512), (2, 37, 5)]:
         n = lib.fl_scan_workspace_bytes(B, T, C)
         chunked3 = B * ((T + 63) // 64) * C * 20
-        lookback = B * ((T + 31) // 32) * ((C + 63) // 64) * 64 * 40  # smallest tiles
+        lookback = B * ((T + 255) // 256) * ((C + 63) // 64) * 64 * 40  # tiles of <= 256 steps
         assert n >= 256 + chunked3 + lookback, (B, T, C, n)
         assert n % 4 == 0
     assert lib.fl_scan_workspace_bytes(0, 2048, 512) == 0
