@@ -99,7 +99,7 @@ def stream_handle(device: torch.device) -> ctypes.c_void_p:
 
 
 # Scan workspaces, one per (device, stream): zero-filled when allocated, then reused as is
-# (the library keeps a launch counter in the first 256 bytes and re-arms it after every call).
+# (the library keeps launch counters in the first 2 KiB and re-arms them after every call).
 _workspaces: dict = {}
 
 
@@ -115,5 +115,7 @@ def scan_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 
 
 def workspace_error(ws: torch.Tensor) -> int:
-    """Error word of a scan workspace header (0 = every look-back wait completed)."""
-    return int(ws[12:16].view(torch.int32).item())
+    """Error word of a scan workspace header (0 = every look-back wait completed).
+
+    Header: bytes 0..3 tiles done, 128..131 error bits, 256.. ticket counters (one per 128 B)."""
+    return int(ws[128:132].view(torch.int32).item())

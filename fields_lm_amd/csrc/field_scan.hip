@@ -541,9 +541,13 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // ------------------------------------------------------------------------------------------
 // Single-pass path (FL_ALGO_LOOKBACK): one launch, raw read once, read written once.
 //
-// Tiles = (chain = (b, channel tile), chunk of W*L steps). Each block takes the next ticket
-// from a counter (so a block only ever waits on tiles whose tickets were taken earlier, by
-// blocks that are already resident: no deadlock); ticket -> tile is chunk-major. A tile
+// Tiles = (chain = (b, channel tile), chunk of W*L steps); ticket -> tile is chunk-major, so the
+// predecessors of ticket t in its chain are t - n_chains, t - 2*n_chains, ... Each block takes
+// its ticket from one of S counters (S divides n_chains, counter = blockIdx mod S, ticket =
+// count*S + counter): a ticket's predecessors share its residue mod S, so they were taken
+// earlier from the same counter, by blocks that are already resident — a block only ever waits
+// on running blocks (no deadlock, whatever the dispatch order), and the S counters (one cache
+// line each) spread the start-of-launch atomics that a single counter would serialise. A tile
 //   1. loads its raw tile into registers and forms the gates;
 //   2. composes its summary (P, B) and publishes it (status AGG);
 //   3. looks back over its chain: the summaries of earlier tiles are composed until a tile
@@ -558,16 +562,23 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // Waits sleep between polls and give up after kSpinLimit polls (error flag set), so every
 // wave terminates.
 // ------------------------------------------------------------------------------------------
+constexpr int kTicketCounters = 8;  // at most S counters
+// Every word sits in its own 128-byte line: counters are hammered by the blocks' first atomic,
+// `done` by their last one.
 struct LookbackHeader {
-  unsigned long long ticket;  // bits 63..32: launch epoch, bits 31..0: next ticket
-  unsigned int done;          // tiles finished in this launch
-  unsigned int error;         // bit 0: a wait hit kSpinLimit; bit 1: ticket out of range
+  unsigned int done;   // tiles finished in this launch
+  unsigned int pad0[31];
+  unsigned int error;  // bit 0: a wait hit kSpinLimit; bit 1: ticket out of range
+  unsigned int pad1[31];
+  // counter x: bits 63..32 launch epoch, bits 31..0 tickets taken in this launch
+  unsigned long long ticket[kTicketCounters][16];
 };
 
 constexpr uint32_t kTagAgg = 1u;
 constexpr uint32_t kTagIncl = 2u;
 constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr size_t kHeaderBytes = 256;
+constexpr size_t kHeaderBytes = 2048;
+static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
 constexpr int kLookbackBatch = 2;  // predecessor summaries fetched per wave per round
 // data planes of a tile: P, Br, Bi (summary), Sr, Si (inclusive state)
 constexpr int kPlanes = 5;
@@ -605,7 +616,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, float* __restrict__ read, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles) {
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   constexpr int kMaxRound = W * kLookbackBatch < 64 ? W * kLookbackBatch : 64;
@@ -619,8 +630,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   if (threadIdx.x == 0) {
-    const unsigned long long tk = atomicAdd(&hdr->ticket, 1ull);
-    s_tk[0] = (uint32_t)tk;
+    const uint32_t x = blockIdx.x % n_split;
+    const unsigned long long tk = atomicAdd(&hdr->ticket[x][0], 1ull);
+    s_tk[0] = (uint32_t)tk * n_split + x;
     s_tk[1] = (uint32_t)(tk >> 32);
   }
   __syncthreads();
@@ -885,13 +897,14 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     }
   }
 
-  // the last block of the launch re-arms the counter for the next launch (next epoch)
+  // the last block of the launch re-arms the counters for the next launch (next epoch)
   if (threadIdx.x == 0) {
     const unsigned int d = atomicAdd(&hdr->done, 1u);
     if (d == n_tiles - 1) {
+      const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
+      for (int x = 0; x < kTicketCounters; ++x)
+        __hip_atomic_store(&hdr->ticket[x][0], armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&hdr->ticket, (unsigned long long)(epoch + 1u) << 32, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -979,7 +992,7 @@ constexpr LookbackTiling kLookbackTilings[] = {
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
 
 // Workspace layout, fixed for a shape whatever the algorithm or tiling:
-//   [header 256 B][status: max tiles x u32][data: max tiles x 5 x CT x u64][chunked3 floats]
+//   [header 2 KiB][status: max tiles x u32][data: max tiles x 5 x CT x u64][chunked3 floats]
 // Status words and data words are only ever written as tagged words (by any tiling), and the
 // three-phase buffers have their own region, so a word left by another call can never carry
 // the current launch's tag.
@@ -1067,11 +1080,19 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
   const WorkspaceLayout lay = workspace_layout(B, T, C);
   char* ws = static_cast<char*>(workspace);
+  // Ticket counters in use: the largest power of two <= kTicketCounters dividing n_chains, for
+  // short chains only. A single counter serialises the blocks' first atomic, which staggers
+  // their start in ticket order; long chains need that stagger for the look-back to keep up
+  // (B=1, T=65,536: 169 us with one counter, 216 us with eight), short chains gain from the
+  // spread (B=8, T=2,048: 38.5 us -> 35.2 us).
+  const int64_t n_chains = B * (int64_t)g.n_ctiles;
+  uint32_t n_split = g.n_chunks <= 64 ? kTicketCounters : 1;
+  while (n_chains % n_split) n_split /= 2;
   fl_scan_lookback_kernel<RawT, K, L, W, OCC><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, read, reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
-      g.n_tiles);
+      g.n_tiles, n_split);
   return hip_status(hipGetLastError());
 }
 

@@ -65,9 +65,9 @@ extern "C" {
  *   state_out  [B, 2C] fp32 planar, or NULL; receives s[T-1]
  *   read       [B, T, 4C] contiguous, read_dtype (FL_DTYPE_F32 only for now)
  *   workspace  device scratch of at least fl_scan_workspace_bytes(B, T, C) bytes, 256-byte
- *              aligned, ZERO-FILLED before its first use and then reused as is: its first 256
- *              bytes hold a launch counter that every call leaves ready for the next one. Calls
- *              on one workspace must be stream-ordered (one workspace per stream).
+ *              aligned, ZERO-FILLED before its first use and then reused as is: its first 2 KiB
+ *              hold launch counters that every call leaves ready for the next one. Calls on one
+ *              workspace must be stream-ordered (one workspace per stream).
  */
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
