@@ -98,17 +98,24 @@ struct RawLoad<bf16_bits, 4> {
   }
 };
 
-// read: buffer store of K floats
-template <int K>
+// read: buffer store of K values as float or as bf16 (round to nearest even, v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t bf16_bits_of(float x) {
+  return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)x);
+}
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  return bf16_bits_of(lo) | (bf16_bits_of(hi) << 16);
+}
+
+template <typename OutT, int K>
 struct ReadStore;
 template <>
-struct ReadStore<1> {
+struct ReadStore<float, 1> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, 0);
   }
 };
 template <>
-struct ReadStore<2> {
+struct ReadStore<float, 2> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
     u32x2 w;
     w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
@@ -116,12 +123,32 @@ struct ReadStore<2> {
   }
 };
 template <>
-struct ReadStore<4> {
+struct ReadStore<float, 4> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
     u32x4 w;
     w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
     w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
     __builtin_amdgcn_raw_buffer_store_b128(w, r, vo, so, 0);
+  }
+};
+template <>
+struct ReadStore<bf16_bits, 1> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)bf16_bits_of(v[0]), r, vo, so, 0);
+  }
+};
+template <>
+struct ReadStore<bf16_bits, 2> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    __builtin_amdgcn_raw_buffer_store_b32(bf16_pair(v[0], v[1]), r, vo, so, 0);
+  }
+};
+template <>
+struct ReadStore<bf16_bits, 4> {
+  __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
+    u32x2 w;
+    w.x = bf16_pair(v[0], v[1]); w.y = bf16_pair(v[2], v[3]);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, 0);
   }
 };
 
@@ -282,6 +309,7 @@ struct WaveTile {
 
   // Recurrence from (sr, si) over the first n steps, storing
   // read[b,t,:] = [Re s | Im s | Re disp | Im disp] (canon:583-621), row j at so0 + j*row_bytes.
+  template <typename OutT>
   __device__ __forceinline__ void materialize(rsrc_t w, int vo, int so0, int row_bytes,
                                               int plane_bytes, int n, const float* lr,
                                               const float* li, float* sr, float* si) const {
@@ -300,10 +328,10 @@ struct WaveTile {
           si[k] = (mi - di[k]) + gbi[j][k];
         }
         const int so = so0 + j * row_bytes;
-        ReadStore<K>::run(w, vo, so, sr);
-        ReadStore<K>::run(w, vo, so + plane_bytes, si);
-        ReadStore<K>::run(w, vo, so + 2 * plane_bytes, dr);
-        ReadStore<K>::run(w, vo, so + 3 * plane_bytes, di);
+        ReadStore<OutT, K>::run(w, vo, so, sr);
+        ReadStore<OutT, K>::run(w, vo, so + plane_bytes, si);
+        ReadStore<OutT, K>::run(w, vo, so + 2 * plane_bytes, dr);
+        ReadStore<OutT, K>::run(w, vo, so + 3 * plane_bytes, di);
       }
     }
   }
@@ -330,21 +358,21 @@ struct TileIo {
   int read_row, read_plane;     // bytes between rows / between the 4 read planes
 };
 
-template <typename RawT>
-__device__ __forceinline__ TileIo tile_io(const RawT* raw, int64_t sb, int64_t st, float* read,
+template <typename RawT, typename OutT>
+__device__ __forceinline__ TileIo tile_io(const RawT* raw, int64_t sb, int64_t st, OutT* read,
                                           int T, int C, int b, int t_begin, int c0) {
   TileIo io;
   const int rows = T - t_begin;  // >= 1
   const RawT* rbase = raw + (int64_t)b * sb + (int64_t)t_begin * st;
   io.raw = make_rsrc(rbase, (uint32_t)(((int64_t)(rows - 1) * st + 3 * (int64_t)C) * sizeof(RawT)));
-  float* wbase = read + ((int64_t)b * T + t_begin) * 4 * C;
-  io.read = make_rsrc(wbase, (uint32_t)((int64_t)rows * 4 * C * sizeof(float)));
+  OutT* wbase = read + ((int64_t)b * T + t_begin) * 4 * C;
+  io.read = make_rsrc(wbase, (uint32_t)((int64_t)rows * 4 * C * sizeof(OutT)));
   io.vo_raw = c0 * (int)sizeof(RawT);
-  io.vo_read = c0 * (int)sizeof(float);
+  io.vo_read = c0 * (int)sizeof(OutT);
   io.raw_row = (int)(st * (int64_t)sizeof(RawT));
   io.raw_plane = C * (int)sizeof(RawT);
-  io.read_row = 4 * C * (int)sizeof(float);
-  io.read_plane = C * (int)sizeof(float);
+  io.read_row = 4 * C * (int)sizeof(OutT);
+  io.read_plane = C * (int)sizeof(OutT);
   return io;
 }
 
@@ -372,7 +400,7 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_summary_kernel(
 
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
-  const TileIo io = tile_io<RawT>(raw, sb, st, nullptr, T, C, b, chunk * kChunkT, c0);
+  const TileIo io = tile_io<RawT, float>(raw, sb, st, nullptr, T, C, b, chunk * kChunkT, c0);
   WaveTile<RawT, K, L> tile;
   tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
   float P[K], Br[K], Bi[K];
@@ -471,11 +499,11 @@ __global__ __launch_bounds__(kCarryWaves * 64) void fl_chunk_carry_kernel(
 }
 
 // Phase 3: re-run each chunk from its carry-in and write read (and state_out).
-template <typename RawT, int K, int L, int W>
+template <typename RawT, typename OutT, int K, int L, int W>
 __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     const float* __restrict__ tr, const float* __restrict__ ti, const float* __restrict__ gamma,
-    const float* __restrict__ carry, float* __restrict__ read, float* __restrict__ state_out) {
+    const float* __restrict__ carry, OutT* __restrict__ read, float* __restrict__ state_out) {
   static_assert(W * L == kChunkT, "chunk length mismatch");
   constexpr int CT = 64 * K;
   __shared__ float s_sum[W][3][CT];
@@ -490,7 +518,7 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
   const int t_begin = chunk * kChunkT;
-  const TileIo io = tile_io<RawT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, c0);
   WaveTile<RawT, K, L> tile;
   tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
   const int n = min(max(T - (t_begin + wave * L), 0), L);  // valid steps of this wave
@@ -527,8 +555,8 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
       }
     }
   }
-  tile.materialize(io.read, io.vo_read, wave * L * io.read_row, io.read_row, io.read_plane, n, lr,
-                   li, sr, si);
+  tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
+                                 io.read_plane, n, lr, li, sr, si);
   if (state_out != nullptr && t_begin + wave * L + n == T) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -610,12 +638,12 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
   }
 }
 
-template <typename RawT, int K, int L, int W, int OCC>
+template <typename RawT, typename OutT, int K, int L, int W, int OCC>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
-    float* __restrict__ state_out, float* __restrict__ read, LookbackHeader* hdr,
+    float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
     uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
@@ -656,7 +684,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
-  const TileIo io = tile_io<RawT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, c0);
   WaveTile<RawT, K, L> tile;
   tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
   const int n_valid = min(max(T - (t_begin + wave * L), 0), L);
@@ -886,8 +914,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
         apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr[k], si[k]);
       }
     }
-    tile.materialize(io.read, io.vo_read, wave * L * io.read_row, io.read_row, io.read_plane,
-                     n_valid, lr, li, sr, si);
+    tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
+                                   io.read_plane, n_valid, lr, li, sr, si);
     if (state_out != nullptr && t_begin + wave * L + n_valid == T) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -1032,10 +1060,10 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t T, int64_t C) {
   return w;
 }
 
-template <typename RawT, int K>
+template <typename RawT, typename OutT, int K>
 int launch_chunked3(const RawT* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
-                    float* state_out, float* read, float* agg, float* carry, hipStream_t stream) {
+                    float* state_out, OutT* read, float* agg, float* carry, hipStream_t stream) {
   constexpr int CT = 64 * K;
   const int n_chunks = (int)cdiv(T, kChunkT);
   const dim3 grid((unsigned)n_chunks, (unsigned)cdiv(C, CT), (unsigned)B);
@@ -1048,34 +1076,35 @@ int launch_chunked3(const RawT* raw, int64_t B, int64_t T, int64_t C, int64_t sb
                                                                  state_in, carry);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
-  fl_chunk_materialize_kernel<RawT, K, 8, 8><<<grid, 8 * 64, 0, stream>>>(
+  fl_chunk_materialize_kernel<RawT, OutT, K, 8, 8><<<grid, 8 * 64, 0, stream>>>(
       raw, sb, st, (int)T, (int)C, n_chunks, tr, ti, gamma, carry, read, state_out);
   return hip_status(hipGetLastError());
 }
 
-template <typename RawT>
+template <typename RawT, typename OutT>
 int dispatch_chunked3(int k, const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb,
                       int64_t st, const float* tr, const float* ti, const float* gamma,
-                      const float* state_in, float* state_out, float* read, float* agg,
+                      const float* state_in, float* state_out, void* read, float* agg,
                       float* carry, hipStream_t stream) {
   const RawT* r = static_cast<const RawT*>(raw);
+  OutT* o = static_cast<OutT*>(read);
   switch (k) {
     case 4:
-      return launch_chunked3<RawT, 4>(r, B, T, C, sb, st, tr, ti, gamma, state_in, state_out,
-                                      read, agg, carry, stream);
+      return launch_chunked3<RawT, OutT, 4>(r, B, T, C, sb, st, tr, ti, gamma, state_in,
+                                            state_out, o, agg, carry, stream);
     case 2:
-      return launch_chunked3<RawT, 2>(r, B, T, C, sb, st, tr, ti, gamma, state_in, state_out,
-                                      read, agg, carry, stream);
+      return launch_chunked3<RawT, OutT, 2>(r, B, T, C, sb, st, tr, ti, gamma, state_in,
+                                            state_out, o, agg, carry, stream);
     default:
-      return launch_chunked3<RawT, 1>(r, B, T, C, sb, st, tr, ti, gamma, state_in, state_out,
-                                      read, agg, carry, stream);
+      return launch_chunked3<RawT, OutT, 1>(r, B, T, C, sb, st, tr, ti, gamma, state_in,
+                                            state_out, o, agg, carry, stream);
   }
 }
 
-template <typename RawT, int K, int L, int W, int OCC>
+template <typename RawT, typename OutT, int K, int L, int W, int OCC>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
-                    float* state_out, float* read, void* workspace, hipStream_t stream) {
+                    float* state_out, void* read, void* workspace, hipStream_t stream) {
   constexpr int CT = 64 * K;
   const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
   const WorkspaceLayout lay = workspace_layout(B, T, C);
@@ -1088,29 +1117,36 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
   uint32_t n_split = g.n_chunks <= 64 ? kTicketCounters : 1;
   while (n_chains % n_split) n_split /= 2;
-  fl_scan_lookback_kernel<RawT, K, L, W, OCC><<<g.n_tiles, W * 64, 0, stream>>>(
+  fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
-      gamma, state_in, state_out, read, reinterpret_cast<LookbackHeader*>(ws),
+      gamma, state_in, state_out, static_cast<OutT*>(read), reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
       g.n_tiles, n_split);
   return hip_status(hipGetLastError());
 }
 
-template <typename RawT>
+template <typename RawT, typename OutT>
 int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T, int64_t C,
                       int64_t sb, int64_t st, const float* tr, const float* ti, const float* gamma,
-                      const float* state_in, float* state_out, float* read, void* ws,
+                      const float* state_in, float* state_out, void* read, void* ws,
                       hipStream_t s) {
-  const LookbackTiling tl = kLookbackTilings[variant];
-  const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
-#define FL_LB(KK, LL, WW, OO)                                                                   \
-  if (kk == KK && tl.l == LL && tl.w == WW && tl.occ == OO)                                      \
-    return launch_lookback<RawT, KK, LL, WW, OO>(raw, B, T, C, sb, st, tr, ti, gamma, state_in, \
-                                                 state_out, read, ws, s);
-  FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 16, 8, 6) FL_LB(1, 32, 4, 4) FL_LB(1, 32, 4, 3)
-  FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4) FL_LB(1, 16, 4, 4)
-  // narrowed K (alignment): same L, W, OCC
-  FL_LB(1, 16, 4, 3) FL_LB(1, 8, 8, 4)
+#define FL_LB(KK, LL, WW, OO)                                                                  \
+  if (kk == KK && tl.l == LL && tl.w == WW && tl.occ == OO)                                     \
+    return launch_lookback<RawT, OutT, KK, LL, WW, OO>(raw, B, T, C, sb, st, tr, ti, gamma,    \
+                                                       state_in, state_out, read, ws, s);
+  if constexpr (sizeof(OutT) == 2) {
+    // bf16 read: the default tiling only (its K = 1 needs no alignment narrowing)
+    const LookbackTiling tl = kLookbackTilings[0];
+    const int kk = tl.k;
+    FL_LB(1, 16, 8, 4)
+  } else {
+    const LookbackTiling tl = kLookbackTilings[variant];
+    const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
+    FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 16, 8, 6) FL_LB(1, 32, 4, 4) FL_LB(1, 32, 4, 3)
+    FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4) FL_LB(1, 16, 4, 4)
+    // narrowed K (alignment): same L, W, OCC
+    FL_LB(1, 16, 4, 3) FL_LB(1, 8, 8, 4)
+  }
 #undef FL_LB
   return FL_ERR_INVALID_ARGUMENT;
 }
@@ -1167,7 +1203,7 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
                        float* state_out, void* read, int read_dtype, void* workspace,
                        size_t workspace_bytes_given, int algo, void* stream) {
   if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
-  if (read_dtype != FL_DTYPE_F32) return FL_ERR_DTYPE;
+  if (read_dtype != FL_DTYPE_F32 && read_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   const int base_algo = algo & 0xff;
   const int variant = algo >> 8;
   if (base_algo != FL_ALGO_AUTO && base_algo != FL_ALGO_CHUNKED3 && base_algo != FL_ALGO_LOOKBACK)
@@ -1179,37 +1215,47 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
   if (B > 1 && raw_stride_b < (T - 1) * raw_stride_t + 3 * C) return FL_ERR_INVALID_ARGUMENT;
   const int64_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
   // per batch row, raw and read rows are addressed through 32-bit buffer offsets
-  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * 4 > kMaxBufferBytes)
+  const int64_t osz = read_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * osz > kMaxBufferBytes)
     return FL_ERR_INVALID_ARGUMENT;
-  if (raw_stride_t * esz > kMaxRowBytes || 4 * C * 4 > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
+  if (raw_stride_t * esz > kMaxRowBytes || 4 * C * osz > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
   if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!raw || !tr || !ti || !gamma || !read) return FL_ERR_INVALID_ARGUMENT;
   const size_t need = workspace_bytes(B, T, C);
   if (!workspace || workspace_bytes_given < need) return FL_ERR_WORKSPACE;
-  if (!aligned(raw, esz) || !aligned(read, 4) || !aligned(workspace, 256))
+  if (!aligned(raw, esz) || !aligned(read, osz) || !aligned(workspace, 256))
     return FL_ERR_INVALID_ARGUMENT;
   if ((state_in && !aligned(state_in, 4)) || (state_out && !aligned(state_out, 4)))
     return FL_ERR_INVALID_ARGUMENT;
 
-  const int k = pick_k(raw_dtype, raw, C, raw_stride_b, raw_stride_t, read, nullptr, nullptr);
+  int k = pick_k(raw_dtype, raw, C, raw_stride_b, raw_stride_t, read, nullptr, nullptr);
+  if (osz == 2) {  // bf16 read: K values are stored as K*2 bytes
+    while (k > 1 && !aligned(read, 2 * k)) k /= 2;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
-  float* rd = static_cast<float*>(read);
+  const bool raw16 = raw_dtype == FL_DTYPE_BF16, out16 = read_dtype == FL_DTYPE_BF16;
   if (base_algo == FL_ALGO_CHUNKED3) {
     const int64_t n_chunks = cdiv(T, kChunkT);
     float* agg = reinterpret_cast<float*>(static_cast<char*>(workspace) +
                                           workspace_layout(B, T, C).chunked3_off);
     float* carry = agg + B * n_chunks * 3 * C;
-    if (raw_dtype == FL_DTYPE_BF16)
-      return dispatch_chunked3<bf16_bits>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti,
-                                          gamma, state_in, state_out, rd, agg, carry, s);
-    return dispatch_chunked3<float>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma,
-                                    state_in, state_out, rd, agg, carry, s);
+#define FL_C3(R, O)                                                                              \
+  return dispatch_chunked3<R, O>(k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma,   \
+                                 state_in, state_out, read, agg, carry, s);
+    if (raw16 && out16) FL_C3(bf16_bits, bf16_bits)
+    if (raw16) FL_C3(bf16_bits, float)
+    if (out16) FL_C3(float, bf16_bits)
+    FL_C3(float, float)
+#undef FL_C3
   }
-  if (raw_dtype == FL_DTYPE_BF16)
-    return dispatch_lookback<bf16_bits>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr,
-                                        ti, gamma, state_in, state_out, rd, workspace, s);
-  return dispatch_lookback<float>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti,
-                                  gamma, state_in, state_out, rd, workspace, s);
+#define FL_LBD(R, O)                                                                          \
+  return dispatch_lookback<R, O>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, \
+                                 gamma, state_in, state_out, read, workspace, s);
+  if (raw16 && out16) FL_LBD(bf16_bits, bf16_bits)
+  if (raw16) FL_LBD(bf16_bits, float)
+  if (out16) FL_LBD(float, bf16_bits)
+  FL_LBD(float, float)
+#undef FL_LBD
 }
 
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,

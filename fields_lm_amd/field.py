@@ -50,13 +50,23 @@ def _check_scan_inputs(raw: torch.Tensor, tr: torch.Tensor):
     return batch, length, channels
 
 
+def _read_code(read_dtype: torch.dtype) -> int:
+    if read_dtype == torch.float32:
+        return nat.FL_DTYPE_F32
+    if read_dtype == torch.bfloat16:
+        return nat.FL_DTYPE_BF16
+    raise TypeError(f"read must be float32 or bfloat16, got {read_dtype}")
+
+
 def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
                gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
-               return_state: bool = False, algo: int = nat.FL_ALGO_AUTO):
-    """Run the HIP scan. Returns ``read`` fp32 [B,T,4C] (and the final planar state [B,2C]).
+               return_state: bool = False, algo: int = nat.FL_ALGO_AUTO,
+               read_dtype: torch.dtype = torch.float32):
+    """Run the HIP scan. Returns ``read`` [B,T,4C] (and the final planar state [B,2C], fp32).
 
     raw: fp32 or bf16 [B,T,3C] on a ROCm device, channel stride 1 (other strides are passed
     through). state_in: fp32 [B,2C] planar (re | im) or None for the zero state.
+    read_dtype: fp32 (the reference's output) or bf16 (the fp32 values rounded to nearest even).
     """
     lib = nat.load()
     batch, length, channels = _check_scan_inputs(raw, transition_r)
@@ -68,7 +78,8 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
     gm = gamma.detach().to(device=dev, dtype=torch.float32).contiguous()
     if ti.numel() != channels or gm.numel() != channels:
         raise ValueError((raw.shape, transition_i.shape, gamma.shape))
-    read = torch.empty((batch, length, 4 * channels), device=dev, dtype=torch.float32)
+    read_code = _read_code(read_dtype)
+    read = torch.empty((batch, length, 4 * channels), device=dev, dtype=read_dtype)
     sin = None
     if state_in is not None:
         if state_in.shape != (batch, 2 * channels):
@@ -84,7 +95,7 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
     code = lib.fl_scan_forward_ex(
         nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels,
         raw.stride(0), raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
-        nat.ptr(sout), nat.ptr(read), nat.FL_DTYPE_F32, nat.ptr(workspace), workspace.numel(), algo,
+        nat.ptr(sout), nat.ptr(read), read_code, nat.ptr(workspace), workspace.numel(), algo,
         nat.stream_handle(dev))
     nat.check(code, "fl_scan_forward")
     return (read, sout) if return_state else read
@@ -94,24 +105,28 @@ class _FieldReadFunction(torch.autograd.Function):
     """Forward of canon:912-1018 on the HIP path. The backward kernels are not built yet."""
 
     @staticmethod
-    def forward(ctx, raw, transition_r, transition_i, gamma, block_c, chunk_t):
-        return field_scan(raw, transition_r, transition_i, gamma)
+    def forward(ctx, raw, transition_r, transition_i, gamma, block_c, chunk_t,
+                read_dtype=torch.float32):
+        return field_scan(raw, transition_r, transition_i, gamma, read_dtype=read_dtype)
 
     @staticmethod
-    def backward(ctx, grad_read):
+    def backward(ctx, *grad_outputs):
         raise NotImplementedError(
             "the HIP Field scan is forward-only: its backward (canon:1020-1105) is not implemented")
 
 
 def fused_field_read(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
-                     gamma: torch.Tensor, block_c: int = 32, chunk_t: int = 64) -> torch.Tensor:
+                     gamma: torch.Tensor, block_c: int = 32, chunk_t: int = 64, *,
+                     read_dtype: torch.dtype = torch.float32) -> torch.Tensor:
     """Drop-in for canon:1108-1123 ``fused_field_read``.
 
     ``block_c`` / ``chunk_t`` are the Triton kernels' tile sizes; they do not change the result
     and are accepted for call compatibility. The HIP kernels choose their own tiling.
-    Unlike the reference, bf16 ``raw`` is accepted as well (upcast in-register, exactly).
+    Unlike the reference, bf16 ``raw`` is accepted as well (upcast in-register, exactly), and
+    ``read_dtype=torch.bfloat16`` returns the same values rounded to bf16.
     """
-    return _FieldReadFunction.apply(raw, transition_r, transition_i, gamma, block_c, chunk_t)
+    return _FieldReadFunction.apply(raw, transition_r, transition_i, gamma, block_c, chunk_t,
+                                    read_dtype)
 
 
 def field_decode_step(raw_t: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
@@ -213,6 +228,9 @@ class IndependentVacancyField(nn.Module):
         self.read_norm = RMSNorm(2 * dim)
         self.out_proj = nn.Linear(2 * dim, dim)
         self.gate_proj = nn.Linear(dim, dim)
+        # "auto": bf16 read when raw is bf16 (bf16 autocast / bf16 weights), else fp32 read;
+        # or a fixed torch dtype. Not a parameter or buffer: state_dict is unchanged.
+        self.read_dtype = "auto"
 
     def transition(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tr, ti, gamma) fp32 [C] (canon:1169-1173), computed in the parameters' dtype."""
@@ -236,9 +254,16 @@ class IndependentVacancyField(nn.Module):
         gate = torch.sigmoid(self.gate_proj(x))
         return x + (out * gate).to(x.dtype)
 
+    def _read_dtype(self, raw: torch.Tensor) -> torch.dtype:
+        if self.read_dtype == "auto":
+            return torch.bfloat16 if raw.dtype == torch.bfloat16 else torch.float32
+        return self.read_dtype
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         tr, ti, gamma = self.transition()
-        read = fused_field_read(self._raw(x), tr, ti, gamma, self.triton_block_c, self.triton_chunk_t)
+        raw = self._raw(x)
+        read = fused_field_read(raw, tr, ti, gamma, self.triton_block_c, self.triton_chunk_t,
+                                read_dtype=self._read_dtype(raw))
         return self._readout(x, read)
 
     def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
@@ -248,7 +273,9 @@ class IndependentVacancyField(nn.Module):
         ``state`` continues a previous segment (state_in); None starts from zero as forward does.
         """
         tr, ti, gamma = self.transition()
-        read, new_state = field_scan(self._raw(x), tr, ti, gamma, state_in=state, return_state=True)
+        raw = self._raw(x)
+        read, new_state = field_scan(raw, tr, ti, gamma, state_in=state, return_state=True,
+                                     read_dtype=self._read_dtype(raw))
         return self._readout(x, read), new_state
 
     def step(self, x_t: torch.Tensor, state: torch.Tensor,
@@ -298,7 +325,7 @@ class ScanPlan:
 
     def __init__(self, raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
                  gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
-                 algo: int = nat.FL_ALGO_AUTO):
+                 algo: int = nat.FL_ALGO_AUTO, read_dtype: torch.dtype = torch.float32):
         self.algo = algo
         self.lib = nat.load()
         batch, length, channels = _check_scan_inputs(raw, transition_r)
@@ -311,13 +338,13 @@ class ScanPlan:
         self.params = [t.detach().to(device=dev, dtype=torch.float32).contiguous()
                        for t in (transition_r, transition_i, gamma)]
         self.state_in = None if state_in is None else state_in.detach().float().contiguous()
-        self.read = torch.empty((batch, length, 4 * channels), device=dev, dtype=torch.float32)
+        self.read = torch.empty((batch, length, 4 * channels), device=dev, dtype=read_dtype)
         self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
         self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
         self.workspace = torch.zeros(self.ws_bytes, device=dev, dtype=torch.uint8)  # zero-filled once
         self.args = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
                      raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
-                     nat.ptr(self.state_out), nat.ptr(self.read), nat.FL_DTYPE_F32,
+                     nat.ptr(self.state_out), nat.ptr(self.read), _read_code(read_dtype),
                      nat.ptr(self.workspace), self.ws_bytes, algo)
         self.device = dev
 

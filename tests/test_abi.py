@@ -76,7 +76,7 @@ def _scan(lib, **kw):
 def test_argument_validation_returns_before_launch(lib):
     # fake (never dereferenced) pointers: every case below fails validation first
     assert _scan(lib, raw_dtype=7) == nat.FL_ERR_DTYPE
-    assert _scan(lib, read_dtype=1) == nat.FL_ERR_DTYPE
+    assert _scan(lib, read_dtype=7) == nat.FL_ERR_DTYPE
     assert _scan(lib, B=0) == nat.FL_ERR_INVALID_ARGUMENT
     assert _scan(lib, T=-1) == nat.FL_ERR_INVALID_ARGUMENT
     assert _scan(lib, st=23) == nat.FL_ERR_INVALID_ARGUMENT

@@ -147,6 +147,29 @@ def test_scan_plan_graph_replays(dev):
     assert nat.workspace_error(plan.workspace) == 0
 
 
+@pytest.mark.parametrize("algo", list(ALGOS))
+def test_bf16_read_is_rounded_fp32_read(dev, algo):
+    """read_dtype=bf16 returns exactly the fp32 result rounded to nearest even (same kernel math)."""
+    from fields_lm_amd import field_scan
+
+    print(f"[case] bf16 read {algo}", flush=True)
+    for (B, T, C, dtype) in [(2, 37, 32, torch.float32), (3, 1000, 512, torch.bfloat16),
+                             (2, 130, 7, torch.bfloat16), (1, 4099, 64, torch.float32)]:
+        g = torch.Generator().manual_seed(B + T + C)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+        sin = torch.randn(B, 2 * C, generator=g) * 0.2
+        tr, ti, gamma = _to(dev, *_params(C, seed=C))
+        draw = raw.to(dev)
+        r32, s32 = field_scan(draw, tr, ti, gamma, state_in=sin.to(dev), return_state=True, algo=ALGOS[algo])
+        r16, s16 = field_scan(draw, tr, ti, gamma, state_in=sin.to(dev), return_state=True, algo=ALGOS[algo],
+                              read_dtype=torch.bfloat16)
+        assert r16.dtype == torch.bfloat16
+        torch.testing.assert_close(r16, r32.to(torch.bfloat16), rtol=0, atol=0)
+        torch.testing.assert_close(s16, s32, rtol=0, atol=0)
+        exp_read, _ = oracle.scan_f64(raw.float(), tr.cpu(), ti.cpu(), gamma.cpu(), state_in=sin)
+        assert oracle.rel_err(r16.float().cpu(), exp_read) <= 4e-3  # bf16 rounding: 2^-9 relative
+
+
 def test_scan_state_in_continuation(dev):
     from fields_lm_amd import field_scan
 

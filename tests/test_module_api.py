@@ -18,8 +18,11 @@ def test_constructor_signatures_match_reference():
         "dim", "backend", "field_chunk", "triton_block_c", "triton_chunk_t"]
     assert list(inspect.signature(FieldBlock.__init__).parameters)[1:] == [
         "dim", "backend", "field_chunk", "triton_block_c", "triton_chunk_t", "ff_hidden"]
-    assert list(inspect.signature(fused_field_read).parameters) == [
-        "raw", "transition_r", "transition_i", "gamma", "block_c", "chunk_t"]
+    params = inspect.signature(fused_field_read).parameters
+    positional = [n for n, p in params.items() if p.kind != inspect.Parameter.KEYWORD_ONLY]
+    assert positional == ["raw", "transition_r", "transition_i", "gamma", "block_c", "chunk_t"]
+    # extensions are keyword-only, so every reference call site binds identically
+    assert all(p.kind == inspect.Parameter.KEYWORD_ONLY for n, p in params.items() if n not in positional)
 
 
 def test_seeded_construction_equals_reference_fixture(golden_dir):
