@@ -580,7 +580,7 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 //   2. composes its summary (P, B) and publishes it (status AGG);
 //   3. looks back over its chain: the summaries of earlier tiles are composed until a tile
 //      with a published inclusive state (status INCL) is found, which gives the carry-in; all
-//      W waves fetch and compose predecessor summaries in parallel, up to kLookbackBatch each
+//      W waves fetch and compose predecessor summaries in parallel, up to kLookbackPerWave each
 //      per round;
 //   4. publishes its inclusive state (status INCL) and materialises.
 // Every published value is a 64-bit word (value | tag), tag = epoch<<2 | kind, written and
@@ -607,7 +607,8 @@ constexpr uint32_t kTagIncl = 2u;
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
-constexpr int kLookbackBatch = 2;  // predecessor summaries fetched per wave per round
+constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
+constexpr int kLookbackPerWave = 8;  // predecessor summaries composed per wave per round
 // data planes of a tile: P, Br, Bi (summary), Sr, Si (inclusive state)
 constexpr int kPlanes = 5;
 
@@ -647,7 +648,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
-  constexpr int kMaxRound = W * kLookbackBatch < 64 ? W * kLookbackBatch : 64;
+  constexpr int kMaxRound = W * kLookbackPerWave < 64 ? W * kLookbackPerWave : 64;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
   __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
   __shared__ float s_part[W][4][CT];  // look-back partial maps (Ar, Ai, Br, Bi)
@@ -780,12 +781,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
         float pAr[K], pAi[K], pBr[K], pBi[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) { pAr[k] = 1.f; pAi[k] = 0.f; pBr[k] = 0.f; pBi[k] = 0.f; }
-        if (ok && hi > lo) {
+        // sub-batches of kLookbackBatch predecessors, nearest first (no barrier in between)
+        for (int q0 = lo; ok && q0 < hi && !failed; q0 += kLookbackBatch) {
           uint64_t w[kLookbackBatch][3][K];
 #pragma unroll
           for (int q = 0; q < kLookbackBatch; ++q) {
-            if (lo + q < hi) {
-              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - lo - q)) * kPlanes * CT + lane * K;
+            if (q0 + q < hi) {
+              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
 #pragma unroll
               for (int k = 0; k < K; ++k) {
                 w[q][0][k] = get_word(dp + k);
@@ -796,8 +798,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
           }
 #pragma unroll
           for (int q = 0; q < kLookbackBatch; ++q) {
-            if (lo + q < hi && !failed) {
-              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - lo - q)) * kPlanes * CT + lane * K;
+            if (q0 + q < hi && !failed) {
+              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
 #pragma unroll
               for (int k = 0; k < K; ++k) {
                 uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
