@@ -751,28 +751,37 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     for (int k = 0; k < K; ++k) { aAr[k] = 1.f; aAi[k] = 0.f; aBr[k] = 0.f; aBi[k] = 0.f; }
     uint32_t spins = 0;
     bool failed = false;
-    int j = chunk - 1;  // nearest predecessor not yet consumed
-    while (true) {
-      if (wave == 0) {
-        const int p = j - lane;
-        uint32_t s = 0;
-        if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
-        const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
-        int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
-        int n;
-        if (i0 >= kMaxRound) {
-          n = kMaxRound;
-          kind = 1;
-        } else {
-          n = i0;
-          const uint32_t s_at = __shfl(s, i0);
-          const int p_at = __shfl(p, i0);
-          kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
-        }
-        if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
+    // Status scan (wave 0): statuses of the 64 predecessors j, j-1, ... in one load; s_meta gets
+    // (j, n, kind): the next round composes the n nearest summaries, then, for kind 2, starts
+    // from the inclusive state of predecessor j-n.
+    auto scan_status = [&](int j) {
+      const int p = j - lane;
+      uint32_t s = 0;
+      if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
+      const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
+      int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
+      int n;
+      if (i0 >= kMaxRound) {
+        n = kMaxRound;
+        kind = 1;
+      } else {
+        n = i0;
+        const uint32_t s_at = __shfl(s, i0);
+        const int p_at = __shfl(p, i0);
+        kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
       }
+      if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
+    };
+    if (wave == 0) {
+      scan_status(chunk - 1);
+      if (lane == 0) s_meta[3] = 0;
+    }
+    // Each round: barrier, every wave composes its share of the n summaries, barrier, wave 0
+    // folds the shares into acc and scans the statuses for the next round.
+    while (true) {
       __syncthreads();
+      if (s_meta[3]) break;
       const int jj = s_meta[0], n = s_meta[1], kind = s_meta[2];
       // this wave composes predecessors jj - i for i in [lo, hi), nearest first
       const int m = (n + W - 1) / W;
@@ -870,13 +879,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
           __builtin_amdgcn_s_sleep(2);
         }
         if (__ballot(failed) != 0ull) done = 1;  // give up: the carry stays state_in / 0
+        if (!done) scan_status(jj - n);
         if (lane == 0) s_meta[3] = done;
       }
-      __syncthreads();
-      const int finished = s_meta[3];
-      if (finished) break;
-      j = jj - n;
-      __syncthreads();  // s_meta is rewritten by the next round
     }
   }
   if (wave == 0) {
