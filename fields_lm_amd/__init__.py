@@ -8,6 +8,7 @@ Public surface (mirrors src/fields_official/reference/field_only_v4_chunked_trit
 * ``fused_field_read(raw, transition_r, transition_i, gamma, block_c, chunk_t)``
 * ``IndependentVacancyField``, ``FieldBlock``, ``RMSNorm``, ``PackedSwiGLU``
 * ``field_scan`` (with state_in / state_out) and ``field_decode_step`` (decode token loop)
+* ``field_scan_norm`` / ``field_decode_norm_step``: the same with the mixer's read_norm fused
 """
 from .field import (  # noqa: F401
     ScanPlan,
@@ -17,8 +18,10 @@ from .field import (  # noqa: F401
     IndependentVacancyField,
     PackedSwiGLU,
     RMSNorm,
+    field_decode_norm_step,
     field_decode_step,
     field_scan,
+    field_scan_norm,
     fused_field_read,
     state_to_complex,
 )

@@ -38,7 +38,11 @@ SIGNATURES = {
     "fl_scan_forward_ex": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                   _vp, _vp, _int, _vp, _sz, _int, _vp]),
     "fl_scan_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "fl_scan_norm_forward": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                                    _vp, _vp, ctypes.c_float, _vp, _int, _vp, _sz, _vp]),
     "fl_decode_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _int, _vp]),
+    "fl_decode_norm_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+                                   ctypes.c_float, _vp, _int, _vp]),
     "fl_version": (ctypes.c_char_p, []),
 }
 

@@ -335,7 +335,94 @@ struct WaveTile {
       }
     }
   }
+
+  // Per step j < n: sum over this lane's K channels of the squares of the four read values
+  // (Re s, Im s, Re disp, Im disp) of the recurrence from (sr0, si0); 0 for j >= n and for
+  // lanes outside the channel range (ok false).
+  __device__ __forceinline__ void sumsq(int n, bool ok, const float* lr, const float* li,
+                                        const float* sr0, const float* si0, float* ss) const {
+    float sr[K], si[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) { sr[k] = sr0[k]; si[k] = si0[k]; }
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      float acc = 0.f;
+      if (j < n) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const float mr = lr[k] * sr[k] - li[k] * si[k];
+          const float mi = lr[k] * si[k] + li[k] * sr[k];
+          const float dr = gv[j][k] * mr, di = gv[j][k] * mi;
+          sr[k] = (mr - dr) + gbr[j][k];
+          si[k] = (mi - di) + gbi[j][k];
+          acc = fmaf(sr[k], sr[k], acc);
+          acc = fmaf(si[k], si[k], acc);
+          acc = fmaf(dr, dr, acc);
+          acc = fmaf(di, di, acc);
+        }
+      }
+      ss[j] = ok ? acc : 0.f;
+    }
+  }
+
+  // materialize() with the RMSNorm epilogue: row j stores (value * scale_j) * nw[plane][k],
+  // scale_j taken from lane j of `scale`. Every lane of the wave runs the recurrence (the
+  // scales are read across lanes); lanes with ok false store nothing.
+  template <typename OutT>
+  __device__ __forceinline__ void materialize_norm(rsrc_t w, int vo, int so0, int row_bytes,
+                                                   int plane_bytes, int n, bool ok,
+                                                   const float* lr, const float* li, float* sr,
+                                                   float* si, float scale,
+                                                   const float (*nw)[K]) const {
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      if (j < n) {
+        const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), j));
+        float o[4][K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const float mr = lr[k] * sr[k] - li[k] * si[k];
+          const float mi = lr[k] * si[k] + li[k] * sr[k];
+          const float dr = gv[j][k] * mr, di = gv[j][k] * mi;
+          sr[k] = (mr - dr) + gbr[j][k];
+          si[k] = (mi - di) + gbi[j][k];
+          o[0][k] = (sr[k] * sc) * nw[0][k];
+          o[1][k] = (si[k] * sc) * nw[1][k];
+          o[2][k] = (dr * sc) * nw[2][k];
+          o[3][k] = (di * sc) * nw[3][k];
+        }
+        if (ok) {
+          const int so = so0 + j * row_bytes;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) ReadStore<OutT, K>::run(w, vo, so + p * plane_bytes, o[p]);
+        }
+      }
+    }
+  }
 };
+
+// Row sums across a wave: v[j] per lane in, lane l out holds the sum over all 64 lanes of
+// v[l mod L]. log2(L) halving exchange stages (each lane keeps the half of its values that
+// its lane bit selects and adds its partner's copy of them), then plain xor stages over the
+// remaining lane bits. L is a power of two <= 64; v is consumed.
+template <int L>
+__device__ __forceinline__ float wave_row_sums(float (&v)[L], int lane) {
+  static_assert(L > 0 && L <= 64 && (L & (L - 1)) == 0, "L must be a power of two <= 64");
+#pragma unroll
+  for (int m = 1; m < L; m <<= 1) {
+    const bool upper = (lane & m) != 0;
+#pragma unroll
+    for (int i = 0; i < L / (2 * m); ++i) {
+      const float keep = upper ? v[2 * i + 1] : v[2 * i];
+      const float give = upper ? v[2 * i] : v[2 * i + 1];
+      v[i] = keep + __shfl_xor(give, m);
+    }
+  }
+  float t = v[0];
+#pragma unroll
+  for (int m = L; m < 64; m <<= 1) t += __shfl_xor(t, m);
+  return t;
+}
 
 template <int K>
 __device__ __forceinline__ void load_params(const float* __restrict__ tr, const float* __restrict__ ti,
@@ -583,6 +670,13 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 //      W waves fetch and compose predecessor summaries in parallel, up to kLookbackPerWave each
 //      per round;
 //   4. publishes its inclusive state (status INCL) and materialises.
+// With the RMSNorm epilogue (NORM), step 4 first runs the tile's recurrence once more without
+// storing, to form each row's partial sum of squares over the tile's channels; publishes the
+// partials (one word per row and channel tile); waits for the partials of the other channel
+// tiles of the same (batch row, chunk) — the n_ctiles consecutive tickets of its group, all
+// taken by blocks that are running or about to run, none of them waiting on this block — and
+// stores read * rsqrt(mean(read^2) + eps) * weight. The inclusive state is published before
+// that wait, so the chain's successors never wait on the exchange.
 // Every published value is a 64-bit word (value | tag), tag = epoch<<2 | kind, written and
 // read with relaxed agent-scope atomics (device-coherent across XCD L2s). A reader checks
 // each word's own tag, so no fences are needed, and the epoch (bumped by the last block of
@@ -604,6 +698,7 @@ struct LookbackHeader {
 
 constexpr uint32_t kTagAgg = 1u;
 constexpr uint32_t kTagIncl = 2u;
+constexpr uint32_t kTagSib = 3u;   // per-row partial sum of squares (NORM epilogue)
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
@@ -639,13 +734,16 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
   }
 }
 
-template <typename RawT, typename OutT, int K, int L, int W, int OCC>
+// NORM: out = RMSNorm(read) (canon:300-309 applied to canon:1176-1193's read), norm_w [4C],
+// sib = per-row partials [n_tiles][W*L] words; otherwise out = read and those are unused.
+template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split,
+    const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   constexpr int kMaxRound = W * kLookbackPerWave < 64 ? W * kLookbackPerWave : 64;
@@ -907,7 +1005,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   }
   __syncthreads();
 
-  if (ok && n_valid > 0) {
+  if (NORM ? n_valid > 0 : (ok && n_valid > 0)) {
     float sr[K], si[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -921,9 +1019,46 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
         apply_map(lLr[k], lLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr[k], si[k]);
       }
     }
-    tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
-                                   io.read_plane, n_valid, lr, li, sr, si);
-    if (state_out != nullptr && t_begin + wave * L + n_valid == T) {
+    if constexpr (NORM) {
+      // partial sums of squares of this tile's rows, lane l holding row l mod L
+      float ss[L];
+      tile.sumsq(n_valid, ok, lr, li, sr, si, ss);
+      const float part = wave_row_sums<L>(ss, lane);
+      const int row = lane & (L - 1);
+      const uint32_t tag_sib = ((epoch & 0x3fffffffu) << 2) | kTagSib;
+      if (lane < L && row < n_valid) put_word(sib + (size_t)ticket * TC + wave * L + row, part, tag_sib);
+      // row totals over the group's channel tiles, summed in the same order by every tile
+      float tot = 0.f;
+      bool sib_failed = false;
+      if (row < n_valid) {
+        uint64_t* sg = sib + ((size_t)chunk * n_chains + (size_t)b * n_ctiles) * TC + wave * L + row;
+        uint32_t spins = 0;
+        for (int s = lane / L; s < n_ctiles; s += 64 / L) {
+          uint64_t w = get_word(sg + (size_t)s * TC);
+          if (!settle_words<1>(sg + (size_t)s * TC, 0, tag_sib, &w, spins)) {
+            sib_failed = true;
+            break;
+          }
+          tot += word_value(w);
+        }
+      }
+#pragma unroll
+      for (int m = L; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
+      if (__ballot(sib_failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
+      const float scale = rsqrtf(fmaf(tot, inv_n, eps));
+      float nw[4][K];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int k = 0; k < K; ++k) nw[p][k] = ok ? norm_w[p * C + c0 + k] : 0.f;
+      tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
+                                           io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
+                                           si, scale, nw);
+    } else {
+      tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
+                                     io.read_plane, n_valid, lr, li, sr, si);
+    }
+    if (ok && state_out != nullptr && t_begin + wave * L + n_valid == T) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         state_out[(int64_t)b * 2 * C + c0 + k] = sr[k];
@@ -991,6 +1126,72 @@ __global__ __launch_bounds__(256) void fl_decode_step_kernel(
   Store<K>::run(o + 3 * C, di);
 }
 
+// Decode step with the RMSNorm epilogue: one block per batch row. Pass 1 forms the row's sum of
+// squares of the four read values over all C channels (state untouched); pass 2 recomputes
+// the step, updates the state in place and stores (value * rsqrt(mean + eps)) * weight. Each
+// channel is owned by one thread in both passes, so the in-place update cannot race.
+constexpr int kDecodeNormThreads = 256;
+
+__device__ __forceinline__ void decode_one(float zr, float zi, float zv, float lr, float li,
+                                           float gm, float& sr, float& si, float& dr, float& di) {
+  float v, br, bi;
+  gates(zr, zi, zv, gm, v, br, bi);
+  const float mr = lr * sr - li * si;
+  const float mi = lr * si + li * sr;
+  dr = v * mr;
+  di = v * mi;
+  sr = (mr - dr) + br;
+  si = (mi - di) + bi;
+}
+
+__device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
+__device__ __forceinline__ void store_out(bf16_bits* p, float v) { *p = (bf16_bits)bf16_bits_of(v); }
+
+template <typename RawT, typename OutT>
+__global__ __launch_bounds__(kDecodeNormThreads) void fl_decode_norm_kernel(
+    const RawT* __restrict__ raw_t, int64_t sb, int C, const float* __restrict__ tr,
+    const float* __restrict__ ti, const float* __restrict__ gamma, float* __restrict__ state,
+    const float* __restrict__ norm_w, float eps, float inv_n, OutT* __restrict__ out_t) {
+  __shared__ float s_red[kDecodeNormThreads / 64];
+  const int b = blockIdx.x;
+  const RawT* p = raw_t + (int64_t)b * sb;
+  float* s = state + (int64_t)b * 2 * C;
+  float acc = 0.f;
+  for (int c = threadIdx.x; c < C; c += kDecodeNormThreads) {
+    float z[3], sr = s[c], si = s[C + c], dr, di;
+    Load<RawT, 1>::run(p + c, &z[0]);
+    Load<RawT, 1>::run(p + C + c, &z[1]);
+    Load<RawT, 1>::run(p + 2 * C + c, &z[2]);
+    decode_one(z[0], z[1], z[2], tr[c], ti[c], gamma[c], sr, si, dr, di);
+    acc = fmaf(sr, sr, acc);
+    acc = fmaf(si, si, acc);
+    acc = fmaf(dr, dr, acc);
+    acc = fmaf(di, di, acc);
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) acc += __shfl_xor(acc, m);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int w = 0; w < kDecodeNormThreads / 64; ++w) tot += s_red[w];
+  const float scale = rsqrtf(fmaf(tot, inv_n, eps));
+  OutT* o = out_t + (int64_t)b * 4 * C;
+  for (int c = threadIdx.x; c < C; c += kDecodeNormThreads) {
+    float z[3], sr = s[c], si = s[C + c], dr, di;
+    Load<RawT, 1>::run(p + c, &z[0]);
+    Load<RawT, 1>::run(p + C + c, &z[1]);
+    Load<RawT, 1>::run(p + 2 * C + c, &z[2]);
+    decode_one(z[0], z[1], z[2], tr[c], ti[c], gamma[c], sr, si, dr, di);
+    s[c] = sr;
+    s[C + c] = si;
+    store_out(o + c, (sr * scale) * norm_w[c]);
+    store_out(o + C + c, (si * scale) * norm_w[C + c]);
+    store_out(o + 2 * C + c, (dr * scale) * norm_w[2 * C + c]);
+    store_out(o + 3 * C + c, (di * scale) * norm_w[3 * C + c]);
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------
@@ -1025,14 +1226,19 @@ constexpr LookbackTiling kLookbackTilings[] = {
     {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4},  {1, 16, 4, 4},
 };
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
+// The RMSNorm epilogue runs with the default tiling only; a group of channel tiles must be
+// resident together, so its size n_ctiles = C/64 is capped (C <= 4096).
+constexpr LookbackTiling kNormTiling = kLookbackTilings[0];
+constexpr int64_t kNormMaxCtiles = 64;
 
 // Workspace layout, fixed for a shape whatever the algorithm or tiling:
-//   [header 2 KiB][status: max tiles x u32][data: max tiles x 5 x CT x u64][chunked3 floats]
+//   [header 2 KiB][status: max tiles x u32][data: max tiles x 5 x CT x u64]
+//   [sib: tiles x TC x u64 of the RMSNorm tiling][chunked3 floats]
 // Status words and data words are only ever written as tagged words (by any tiling), and the
 // three-phase buffers have their own region, so a word left by another call can never carry
 // the current launch's tag.
 struct WorkspaceLayout {
-  size_t status_off, data_off, chunked3_off, bytes;
+  size_t status_off, data_off, sib_off, chunked3_off, bytes;
 };
 
 struct LookbackGeom {
@@ -1062,7 +1268,12 @@ WorkspaceLayout workspace_layout(int64_t B, int64_t T, int64_t C) {
   WorkspaceLayout w;
   w.status_off = kHeaderBytes;
   w.data_off = w.status_off + (size_t)cdiv((int64_t)max_tiles * 4, 256) * 256;
-  w.chunked3_off = w.data_off + (size_t)cdiv((int64_t)max_data, 256) * 256;
+  w.sib_off = w.data_off + (size_t)cdiv((int64_t)max_data, 256) * 256;
+  {
+    const LookbackTiling tl = kNormTiling;
+    const LookbackGeom g = lookback_geom(B, T, C, 64 * tl.k, tl.l * tl.w);
+    w.chunked3_off = w.sib_off + (size_t)cdiv((int64_t)g.n_tiles * tl.l * tl.w * 8, 256) * 256;
+  }
   w.bytes = w.chunked3_off + (size_t)(B * cdiv(T, kChunkT) * C) * 5 * sizeof(float);
   return w;
 }
@@ -1108,10 +1319,16 @@ int dispatch_chunked3(int k, const void* raw, int64_t B, int64_t T, int64_t C, i
   }
 }
 
-template <typename RawT, typename OutT, int K, int L, int W, int OCC>
+struct NormArgs {
+  const float* weight;  // [4C], nullptr: no epilogue
+  float eps;
+};
+
+template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
-                    float* state_out, void* read, void* workspace, hipStream_t stream) {
+                    float* state_out, void* read, void* workspace, NormArgs norm,
+                    hipStream_t stream) {
   constexpr int CT = 64 * K;
   const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
   const WorkspaceLayout lay = workspace_layout(B, T, C);
@@ -1124,11 +1341,12 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
   uint32_t n_split = g.n_chunks <= 64 ? kTicketCounters : 1;
   while (n_chains % n_split) n_split /= 2;
-  fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC><<<g.n_tiles, W * 64, 0, stream>>>(
+  fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
-      g.n_tiles, n_split);
+      g.n_tiles, n_split, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)),
+      reinterpret_cast<uint64_t*>(ws + lay.sib_off));
   return hip_status(hipGetLastError());
 }
 
@@ -1136,11 +1354,18 @@ template <typename RawT, typename OutT>
 int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T, int64_t C,
                       int64_t sb, int64_t st, const float* tr, const float* ti, const float* gamma,
                       const float* state_in, float* state_out, void* read, void* ws,
-                      hipStream_t s) {
+                      NormArgs norm, hipStream_t s) {
 #define FL_LB(KK, LL, WW, OO)                                                                  \
   if (kk == KK && tl.l == LL && tl.w == WW && tl.occ == OO)                                     \
-    return launch_lookback<RawT, OutT, KK, LL, WW, OO>(raw, B, T, C, sb, st, tr, ti, gamma,    \
-                                                       state_in, state_out, read, ws, s);
+    return launch_lookback<RawT, OutT, KK, LL, WW, OO, false>(raw, B, T, C, sb, st, tr, ti,    \
+                                                              gamma, state_in, state_out, read, \
+                                                              ws, norm, s);
+  if (norm.weight != nullptr) {  // RMSNorm epilogue: the default tiling (K = 1, no narrowing)
+    constexpr LookbackTiling tl = kNormTiling;
+    static_assert(tl.k == 1, "the RMSNorm tiling must not need alignment narrowing");
+    return launch_lookback<RawT, OutT, tl.k, tl.l, tl.w, tl.occ, true>(
+        raw, B, T, C, sb, st, tr, ti, gamma, state_in, state_out, read, ws, norm, s);
+  }
   if constexpr (sizeof(OutT) == 2) {
     // bf16 read: the default tiling only (its K = 1 needs no alignment narrowing)
     const LookbackTiling tl = kLookbackTilings[0];
@@ -1204,11 +1429,15 @@ const char* fl_version(void) { return "fields_amd 0.3 gfx950"; }
 
 size_t fl_scan_workspace_bytes(int64_t B, int64_t T, int64_t C) { return workspace_bytes(B, T, C); }
 
-int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
-                       int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
-                       const float* ti, const float* gamma, const float* state_in,
-                       float* state_out, void* read, int read_dtype, void* workspace,
-                       size_t workspace_bytes_given, int algo, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+              int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
+              const float* gamma, const float* state_in, float* state_out, void* read,
+              int read_dtype, void* workspace, size_t workspace_bytes_given, int algo,
+              NormArgs norm, void* stream) {
   if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   if (read_dtype != FL_DTYPE_F32 && read_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   const int base_algo = algo & 0xff;
@@ -1234,6 +1463,13 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
     return FL_ERR_INVALID_ARGUMENT;
   if ((state_in && !aligned(state_in, 4)) || (state_out && !aligned(state_out, 4)))
     return FL_ERR_INVALID_ARGUMENT;
+  if (norm.weight != nullptr) {
+    // the epilogue exists on the look-back path only; a group of C/64 channel tiles must be
+    // resident together
+    if (base_algo == FL_ALGO_CHUNKED3 || variant != 0) return FL_ERR_INVALID_ARGUMENT;
+    if (cdiv(C, 64 * kNormTiling.k) > kNormMaxCtiles) return FL_ERR_INVALID_ARGUMENT;
+    if (!aligned(norm.weight, 4) || !(norm.eps >= 0.f)) return FL_ERR_INVALID_ARGUMENT;
+  }
 
   int k = pick_k(raw_dtype, raw, C, raw_stride_b, raw_stride_t, read, nullptr, nullptr);
   if (osz == 2) {  // bf16 read: K values are stored as K*2 bytes
@@ -1257,12 +1493,38 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
   }
 #define FL_LBD(R, O)                                                                          \
   return dispatch_lookback<R, O>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, \
-                                 gamma, state_in, state_out, read, workspace, s);
+                                 gamma, state_in, state_out, read, workspace, norm, s);
   if (raw16 && out16) FL_LBD(bf16_bits, bf16_bits)
   if (raw16) FL_LBD(bf16_bits, float)
   if (out16) FL_LBD(float, bf16_bits)
   FL_LBD(float, float)
 #undef FL_LBD
+}
+
+}  // namespace
+
+extern "C" {
+
+int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                       int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                       const float* ti, const float* gamma, const float* state_in,
+                       float* state_out, void* read, int read_dtype, void* workspace,
+                       size_t workspace_bytes_given, int algo, void* stream) {
+  return scan_impl(raw, raw_dtype, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in,
+                   state_out, read, read_dtype, workspace, workspace_bytes_given, algo,
+                   NormArgs{nullptr, 0.f}, stream);
+}
+
+int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                         int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                         const float* ti, const float* gamma, const float* state_in,
+                         float* state_out, const float* norm_weight, float eps, void* out,
+                         int out_dtype, void* workspace, size_t workspace_bytes_given,
+                         void* stream) {
+  if (norm_weight == nullptr) return FL_ERR_INVALID_ARGUMENT;
+  return scan_impl(raw, raw_dtype, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in,
+                   state_out, out, out_dtype, workspace, workspace_bytes_given, FL_ALGO_LOOKBACK,
+                   NormArgs{norm_weight, eps}, stream);
 }
 
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
@@ -1294,6 +1556,37 @@ int fl_decode_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C, int64
   if (raw_dtype == FL_DTYPE_BF16)
     return dispatch_decode<bf16_bits>(k, raw_t, B, C, raw_stride_b, tr, ti, gamma, state, rd, s);
   return dispatch_decode<float>(k, raw_t, B, C, raw_stride_b, tr, ti, gamma, state, rd, s);
+}
+
+int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
+                        int64_t raw_stride_b, const float* tr, const float* ti,
+                        const float* gamma, float* state, const float* norm_weight, float eps,
+                        void* out_t, int out_dtype, void* stream) {
+  if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
+  if (out_dtype != FL_DTYPE_F32 && out_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
+  if (B <= 0 || C <= 0 || B > kMaxB || C > kMaxC) return FL_ERR_INVALID_ARGUMENT;
+  if (raw_stride_b < 3 * C) return FL_ERR_INVALID_ARGUMENT;
+  if (!raw_t || !tr || !ti || !gamma || !state || !norm_weight || !out_t)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (!(eps >= 0.f)) return FL_ERR_INVALID_ARGUMENT;
+  const size_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  const size_t osz = out_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  if (!aligned(raw_t, esz) || !aligned(state, 4) || !aligned(out_t, osz) ||
+      !aligned(norm_weight, 4) || !aligned(tr, 4) || !aligned(ti, 4) || !aligned(gamma, 4))
+    return FL_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float inv_n = (float)(1.0 / (4.0 * (double)C));
+#define FL_DN(R, O)                                                                             \
+  fl_decode_norm_kernel<R, O><<<(unsigned)B, kDecodeNormThreads, 0, s>>>(                        \
+      static_cast<const R*>(raw_t), raw_stride_b, (int)C, tr, ti, gamma, state, norm_weight, eps, \
+      inv_n, static_cast<O*>(out_t));                                                            \
+  return hip_status(hipGetLastError());
+  const bool raw16 = raw_dtype == FL_DTYPE_BF16, out16 = out_dtype == FL_DTYPE_BF16;
+  if (raw16 && out16) { FL_DN(bf16_bits, bf16_bits) }
+  if (raw16) { FL_DN(bf16_bits, float) }
+  if (out16) { FL_DN(float, bf16_bits) }
+  FL_DN(float, float)
+#undef FL_DN
 }
 
 }  // extern "C"

@@ -3,7 +3,10 @@
 Reference: src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py ("canon").
 
 * :func:`fused_field_read`      — same call as canon:1108-1123; runs ``fl_scan_forward``.
-* :func:`field_decode_step`     — single-token step (no reference counterpart), ``fl_decode_step``.
+* :func:`field_scan_norm`       — the scan with the mixer's read_norm fused in (canon:1176-1193
+  then canon:300-309), ``fl_scan_norm_forward``.
+* :func:`field_decode_step`     — single-token step (no reference counterpart), ``fl_decode_step``;
+  :func:`field_decode_norm_step` the same with read_norm fused, ``fl_decode_norm_step``.
 * :class:`IndependentVacancyField`, :class:`FieldBlock`, :class:`RMSNorm`,
   :class:`PackedSwiGLU` — same constructor signatures, parameter names, initialisation order
   and forward maths as canon:1131-1221 and canon:300-325, so a reference state_dict loads
@@ -58,16 +61,10 @@ def _read_code(read_dtype: torch.dtype) -> int:
     raise TypeError(f"read must be float32 or bfloat16, got {read_dtype}")
 
 
-def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
-               gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
-               return_state: bool = False, algo: int = nat.FL_ALGO_AUTO,
-               read_dtype: torch.dtype = torch.float32):
-    """Run the HIP scan. Returns ``read`` [B,T,4C] (and the final planar state [B,2C], fp32).
+def _scan_call(raw, transition_r, transition_i, gamma, state_in, return_state, out_dtype, launch):
+    """Shared argument handling of the scan entry points; ``launch(lib, args)`` makes the call.
 
-    raw: fp32 or bf16 [B,T,3C] on a ROCm device, channel stride 1 (other strides are passed
-    through). state_in: fp32 [B,2C] planar (re | im) or None for the zero state.
-    read_dtype: fp32 (the reference's output) or bf16 (the fp32 values rounded to nearest even).
-    """
+    args = (raw, batch, length, channels, tr, ti, gm, sin, sout, out, workspace)."""
     lib = nat.load()
     batch, length, channels = _check_scan_inputs(raw, transition_r)
     if raw.stride(2) != 1:
@@ -78,8 +75,8 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
     gm = gamma.detach().to(device=dev, dtype=torch.float32).contiguous()
     if ti.numel() != channels or gm.numel() != channels:
         raise ValueError((raw.shape, transition_i.shape, gamma.shape))
-    read_code = _read_code(read_dtype)
-    read = torch.empty((batch, length, 4 * channels), device=dev, dtype=read_dtype)
+    _read_code(out_dtype)
+    out = torch.empty((batch, length, 4 * channels), device=dev, dtype=out_dtype)
     sin = None
     if state_in is not None:
         if state_in.shape != (batch, 2 * channels):
@@ -89,16 +86,68 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
     if batch == 0 or length == 0 or channels == 0:
         if sout is not None:
             sout.copy_(sin if sin is not None else torch.zeros_like(sout))
-        return (read, sout) if return_state else read
+        return (out, sout) if return_state else out
     ws_bytes = int(lib.fl_scan_workspace_bytes(batch, length, channels))
     workspace = nat.scan_workspace(dev, ws_bytes)
-    code = lib.fl_scan_forward_ex(
-        nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels,
-        raw.stride(0), raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
-        nat.ptr(sout), nat.ptr(read), read_code, nat.ptr(workspace), workspace.numel(), algo,
-        nat.stream_handle(dev))
-    nat.check(code, "fl_scan_forward")
-    return (read, sout) if return_state else read
+    launch(lib, (raw, batch, length, channels, tr, ti, gm, sin, sout, out, workspace))
+    return (out, sout) if return_state else out
+
+
+def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+               gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
+               return_state: bool = False, algo: int = nat.FL_ALGO_AUTO,
+               read_dtype: torch.dtype = torch.float32):
+    """Run the HIP scan. Returns ``read`` [B,T,4C] (and the final planar state [B,2C], fp32).
+
+    raw: fp32 or bf16 [B,T,3C] on a ROCm device, channel stride 1 (other strides are passed
+    through). state_in: fp32 [B,2C] planar (re | im) or None for the zero state.
+    read_dtype: fp32 (the reference's output) or bf16 (the fp32 values rounded to nearest even).
+    """
+    def launch(lib, a):
+        raw_, batch, length, channels, tr, ti, gm, sin, sout, read, ws = a
+        code = lib.fl_scan_forward_ex(
+            nat.ptr(raw_), nat.dtype_code(raw_.dtype), batch, length, channels,
+            raw_.stride(0), raw_.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
+            nat.ptr(sout), nat.ptr(read), _read_code(read.dtype), nat.ptr(ws), ws.numel(), algo,
+            nat.stream_handle(raw_.device))
+        nat.check(code, "fl_scan_forward")
+
+    return _scan_call(raw, transition_r, transition_i, gamma, state_in, return_state, read_dtype,
+                      launch)
+
+
+def _norm_weight(weight: torch.Tensor, channels: int, device) -> torch.Tensor:
+    w = weight.detach().to(device=device, dtype=torch.float32).contiguous()
+    if w.numel() != 4 * channels:
+        raise ValueError(f"norm weight must have 4C = {4 * channels} entries, got {w.numel()}")
+    return w
+
+
+def field_scan_norm(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+                    gamma: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                    state_in: Optional[torch.Tensor] = None, return_state: bool = False,
+                    out_dtype: torch.dtype = torch.float32):
+    """``RMSNorm(read)`` of the scan in one launch (canon:1176-1193 then canon:300-309):
+    out[b,t,:] = read * rsqrt(mean(read^2) + eps) * weight, with read in fp32 as
+    :func:`field_scan` computes it; ``read`` itself is never written to memory.
+
+    weight: [4C] (the mixer's ``read_norm.weight``). out_dtype fp32, or bf16 (the fp32 value
+    rounded to nearest even, as bf16 autocast hands it to out_proj). C <= 4096.
+    """
+    def launch(lib, a):
+        raw_, batch, length, channels, tr, ti, gm, sin, sout, out, ws = a
+        w = _norm_weight(weight, channels, raw_.device)
+        code = lib.fl_scan_norm_forward(
+            nat.ptr(raw_), nat.dtype_code(raw_.dtype), batch, length, channels,
+            raw_.stride(0), raw_.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin),
+            nat.ptr(sout), nat.ptr(w), ctypes.c_float(float(eps)), nat.ptr(out),
+            _read_code(out.dtype), nat.ptr(ws), ws.numel(), nat.stream_handle(raw_.device))
+        nat.check(code, "fl_scan_norm_forward")
+
+    if raw.is_cuda:
+        _norm_weight(weight, raw.shape[-1] // 3, raw.device)  # shape check before any launch
+    return _scan_call(raw, transition_r, transition_i, gamma, state_in, return_state, out_dtype,
+                      launch)
 
 
 class _FieldReadFunction(torch.autograd.Function):
@@ -108,6 +157,20 @@ class _FieldReadFunction(torch.autograd.Function):
     def forward(ctx, raw, transition_r, transition_i, gamma, block_c, chunk_t,
                 read_dtype=torch.float32):
         return field_scan(raw, transition_r, transition_i, gamma, read_dtype=read_dtype)
+
+    @staticmethod
+    def backward(ctx, *grad_outputs):
+        raise NotImplementedError(
+            "the HIP Field scan is forward-only: its backward (canon:1020-1105) is not implemented")
+
+
+class _FieldNormReadFunction(torch.autograd.Function):
+    """Forward of read_norm(fused_field_read(...)) on the HIP path; no backward yet."""
+
+    @staticmethod
+    def forward(ctx, raw, transition_r, transition_i, gamma, weight, eps, out_dtype):
+        return field_scan_norm(raw, transition_r, transition_i, gamma, weight, eps,
+                               out_dtype=out_dtype)
 
     @staticmethod
     def backward(ctx, *grad_outputs):
@@ -159,6 +222,43 @@ def field_decode_step(raw_t: torch.Tensor, transition_r: torch.Tensor, transitio
                               nat.ptr(gamma), nat.ptr(state), nat.ptr(out), nat.FL_DTYPE_F32,
                               nat.stream_handle(raw_t.device))
     nat.check(code, "fl_decode_step")
+    return out
+
+
+def field_decode_norm_step(raw_t: torch.Tensor, transition_r: torch.Tensor,
+                           transition_i: torch.Tensor, gamma: torch.Tensor, state: torch.Tensor,
+                           weight: torch.Tensor, eps: float = 1e-6,
+                           out: Optional[torch.Tensor] = None,
+                           out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """:func:`field_decode_step` with read_norm fused: ``state`` advances in place and the
+    result is RMSNorm(read_t) [B,4C] (``weight`` [4C] fp32 on the device). Capturable."""
+    lib = nat.load()
+    if not raw_t.is_cuda:
+        raise RuntimeError("Field decode step requires a ROCm (cuda) device")
+    if raw_t.ndim != 2 or raw_t.shape[1] % 3:
+        raise ValueError(raw_t.shape)
+    batch, channels = raw_t.shape[0], raw_t.shape[1] // 3
+    if transition_r.numel() != channels:
+        raise ValueError((raw_t.shape, transition_r.shape))
+    if raw_t.stride(1) != 1:
+        raw_t = raw_t.contiguous()
+    if state.shape != (batch, 2 * channels) or state.dtype != torch.float32 or not state.is_contiguous():
+        raise ValueError("state must be a contiguous fp32 [B, 2C] tensor")
+    for p in (transition_r, transition_i, gamma, weight):
+        if p.dtype != torch.float32 or not p.is_contiguous() or p.device != raw_t.device:
+            raise ValueError("transition_r/transition_i/gamma/weight must be contiguous fp32 on the raw device")
+    if weight.numel() != 4 * channels:
+        raise ValueError(f"norm weight must have 4C = {4 * channels} entries, got {weight.numel()}")
+    if out is None:
+        out = torch.empty((batch, 4 * channels), device=raw_t.device, dtype=out_dtype)
+    if out.shape != (batch, 4 * channels) or not out.is_contiguous():
+        raise ValueError("out must be a contiguous [B, 4C] tensor")
+    code = lib.fl_decode_norm_step(nat.ptr(raw_t), nat.dtype_code(raw_t.dtype), batch, channels,
+                                   raw_t.stride(0), nat.ptr(transition_r), nat.ptr(transition_i),
+                                   nat.ptr(gamma), nat.ptr(state), nat.ptr(weight),
+                                   ctypes.c_float(float(eps)), nat.ptr(out), _read_code(out.dtype),
+                                   nat.stream_handle(raw_t.device))
+    nat.check(code, "fl_decode_norm_step")
     return out
 
 
@@ -228,9 +328,14 @@ class IndependentVacancyField(nn.Module):
         self.read_norm = RMSNorm(2 * dim)
         self.out_proj = nn.Linear(2 * dim, dim)
         self.gate_proj = nn.Linear(dim, dim)
-        # "auto": bf16 read when raw is bf16 (bf16 autocast / bf16 weights), else fp32 read;
-        # or a fixed torch dtype. Not a parameter or buffer: state_dict is unchanged.
+        # dtype of what the scan hands to out_proj. "auto": bf16 when raw is bf16 (bf16
+        # autocast, whose out_proj casts its input to bf16 anyway), else fp32; or a fixed
+        # torch dtype. Not a parameter or buffer: state_dict is unchanged.
         self.read_dtype = "auto"
+        # True: read_norm runs inside the scan kernel (fl_scan_norm_forward /
+        # fl_decode_norm_step) and the fp32 read never reaches memory; False: the scan writes
+        # read and read_norm runs as a separate module call, as in the reference.
+        self.fuse_read_norm = True
 
     def transition(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tr, ti, gamma) fp32 [C] (canon:1169-1173), computed in the parameters' dtype."""
@@ -250,9 +355,15 @@ class IndependentVacancyField(nn.Module):
         return raw
 
     def _readout(self, x: torch.Tensor, read: torch.Tensor) -> torch.Tensor:
-        out = self.out_proj(self.read_norm(read))
+        return self._project(x, self.read_norm(read))
+
+    def _project(self, x: torch.Tensor, normed: torch.Tensor) -> torch.Tensor:
+        out = self.out_proj(normed)
         gate = torch.sigmoid(self.gate_proj(x))
         return x + (out * gate).to(x.dtype)
+
+    def _fused(self) -> bool:
+        return self.fuse_read_norm and type(self.read_norm) is RMSNorm and self.channels <= 4096
 
     def _read_dtype(self, raw: torch.Tensor) -> torch.dtype:
         if self.read_dtype == "auto":
@@ -262,6 +373,10 @@ class IndependentVacancyField(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         tr, ti, gamma = self.transition()
         raw = self._raw(x)
+        if self._fused():
+            normed = _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
+                                                  self.read_norm.eps, self._read_dtype(raw))
+            return self._project(x, normed)
         read = fused_field_read(raw, tr, ti, gamma, self.triton_block_c, self.triton_chunk_t,
                                 read_dtype=self._read_dtype(raw))
         return self._readout(x, read)
@@ -274,6 +389,11 @@ class IndependentVacancyField(nn.Module):
         """
         tr, ti, gamma = self.transition()
         raw = self._raw(x)
+        if self._fused():
+            normed, new_state = field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight,
+                                                self.read_norm.eps, state_in=state,
+                                                return_state=True, out_dtype=self._read_dtype(raw))
+            return self._project(x, normed), new_state
         read, new_state = field_scan(raw, tr, ti, gamma, state_in=state, return_state=True,
                                      read_dtype=self._read_dtype(raw))
         return self._readout(x, read), new_state
@@ -285,7 +405,13 @@ class IndependentVacancyField(nn.Module):
         ``params`` = a cached ``self.transition()`` (recomputed when None).
         """
         tr, ti, gamma = params if params is not None else self.transition()
-        read_t = field_decode_step(self._raw(x_t), tr, ti, gamma, state)
+        raw_t = self._raw(x_t)
+        if self._fused():
+            w = self.read_norm.weight.detach().float().contiguous()
+            normed = field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
+                                            out_dtype=self._read_dtype(raw_t))
+            return self._project(x_t, normed)
+        read_t = field_decode_step(raw_t, tr, ti, gamma, state)
         return self._readout(x_t, read_t)
 
     def new_state(self, batch: int, device=None) -> torch.Tensor:
@@ -321,11 +447,13 @@ class ScanPlan:
     allocated once, so :meth:`run` is one C call (no allocation; capturable in a HIP graph).
 
     ``raw`` may be refilled in place between runs; ``read`` and ``state_out`` are overwritten.
+    With ``norm_weight`` [4C], ``read`` receives RMSNorm(read) (``fl_scan_norm_forward``).
     """
 
     def __init__(self, raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
                  gamma: torch.Tensor, state_in: Optional[torch.Tensor] = None,
-                 algo: int = nat.FL_ALGO_AUTO, read_dtype: torch.dtype = torch.float32):
+                 algo: int = nat.FL_ALGO_AUTO, read_dtype: torch.dtype = torch.float32,
+                 norm_weight: Optional[torch.Tensor] = None, eps: float = 1e-6):
         self.algo = algo
         self.lib = nat.load()
         batch, length, channels = _check_scan_inputs(raw, transition_r)
@@ -342,14 +470,24 @@ class ScanPlan:
         self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
         self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
         self.workspace = torch.zeros(self.ws_bytes, device=dev, dtype=torch.uint8)  # zero-filled once
-        self.args = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
-                     raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
-                     nat.ptr(self.state_out), nat.ptr(self.read), _read_code(read_dtype),
-                     nat.ptr(self.workspace), self.ws_bytes, algo)
+        head = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
+                raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
+                nat.ptr(self.state_out))
+        if norm_weight is None:
+            self.norm_weight = None
+            self.fn, self.name = self.lib.fl_scan_forward_ex, "fl_scan_forward"
+            self.args = head + (nat.ptr(self.read), _read_code(read_dtype), nat.ptr(self.workspace),
+                                self.ws_bytes, algo)
+        else:
+            self.norm_weight = _norm_weight(norm_weight, channels, dev)
+            self.fn, self.name = self.lib.fl_scan_norm_forward, "fl_scan_norm_forward"
+            self.args = head + (nat.ptr(self.norm_weight), ctypes.c_float(float(eps)),
+                                nat.ptr(self.read), _read_code(read_dtype), nat.ptr(self.workspace),
+                                self.ws_bytes)
         self.device = dev
 
     def run(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
-        code = self.lib.fl_scan_forward_ex(*self.args, ctypes.c_void_p(s.cuda_stream))
-        nat.check(code, "fl_scan_forward")
+        code = self.fn(*self.args, ctypes.c_void_p(s.cuda_stream))
+        nat.check(code, self.name)
         return self.read

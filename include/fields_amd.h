@@ -83,6 +83,26 @@ int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int
                        size_t workspace_bytes, int algo, void* stream);
 
 /*
+ * Forward scan with the mixer's read_norm RMSNorm fused into the epilogue: writes
+ *
+ *   out[b,t,j] = (read[b,t,j] * rsqrt(sum_i read[b,t,i]^2 / (4C) + eps)) * norm_weight[j]
+ *
+ * for the read that fl_scan_forward computes (in fp32), without writing read itself. Replaces
+ * `self.read_norm(fused_field_read(...))` in `IndependentVacancyField.forward`
+ * (field_only_v4_chunked_triton_wiki100.py:1176-1193, RMSNorm 300-309); the out_proj GEMM
+ * then reads `out` directly. out_dtype FL_DTYPE_BF16 gives the fp32 value rounded to nearest
+ * even, which is what the reference's out_proj sees under bf16 autocast.
+ *
+ * Arguments as fl_scan_forward, plus norm_weight [4C] fp32 and eps (>= 0); the same workspace.
+ * Single-launch path only; C <= 4096.
+ */
+int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                         int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                         const float* ti, const float* gamma, const float* state_in,
+                         float* state_out, const float* norm_weight, float eps, void* out,
+                         int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Workspace size in bytes for fl_scan_forward at this shape (host function, no device call).
  * Replaces the six [B, n_chunks, C] fp32 torch.empty buffers of
  * field_only_v4_chunked_triton_wiki100.py:941-952.
@@ -99,11 +119,22 @@ size_t fl_scan_workspace_bytes(int64_t B, int64_t T, int64_t C);
  *
  *   raw_t  [B, 3C] of raw_dtype, row stride raw_stride_b elements (>= 3C), channel stride 1
  *   state  [B, 2C] fp32 planar, updated in place
- *   read_t [B, 4C] contiguous, read_dtype (FL_DTYPE_F32 only for now)
+ *   read_t [B, 4C] contiguous, read_dtype FL_DTYPE_F32
  */
 int fl_decode_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C, int64_t raw_stride_b,
                    const float* tr, const float* ti, const float* gamma, float* state,
                    void* read_t, int read_dtype, void* stream);
+
+/*
+ * fl_decode_step with the read_norm RMSNorm fused in: state advances as in fl_decode_step and
+ * out_t [B, 4C] (out_dtype F32 or BF16, contiguous) receives the normalised read_t, as
+ * fl_scan_norm_forward defines it. The decode-loop counterpart of fl_scan_norm_forward
+ * (field_only_v4_chunked_triton_wiki100.py:1176-1193 and 300-309 for one token).
+ */
+int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
+                        int64_t raw_stride_b, const float* tr, const float* ti,
+                        const float* gamma, float* state, const float* norm_weight, float eps,
+                        void* out_t, int out_dtype, void* stream);
 
 /* Library version string (host function). No counterpart in the reference. */
 const char* fl_version(void);

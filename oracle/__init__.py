@@ -9,6 +9,8 @@ Contents
 * :func:`scan_f64` / :func:`decode_step_f64` — float64 sequential recurrence in plain C
   (``field_oracle.c``), following ``reference_field_read``
   (src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py:392-416).
+* :func:`rms_norm_f64` — float64 ``RMSNorm`` (same file, 300-309), the mixer's ``read_norm``
+  applied to ``read`` (1193): the checker of the fused scan epilogue.
 * :mod:`oracle.reference_path` — op-for-op torch restatement of the reference's CPU path
   (``assoc_scan`` / ``hierarchical_scan`` / ``reference_field_read``, same file 333-416) and of
   the Field mixer / block forward (1131-1221, 300-325). Also the timed CPU baseline.
@@ -109,6 +111,19 @@ def decode_step_f64(raw_t, tr, ti, gamma, state) -> Tuple[np.ndarray, np.ndarray
     lib.fo_decode_step_f64(_ptr(raw_t), B, C, C3, _ptr(_f64(tr)), _ptr(_f64(ti)), _ptr(_f64(gamma)),
                            _ptr(st), _ptr(out))
     return out, st
+
+
+def rms_norm_f64(x, weight, eps: float = 1e-6) -> np.ndarray:
+    """float64 RMSNorm over the last axis: x * (mean(x^2) + eps)^(-1/2) * weight.
+
+    Follows ``RMSNorm.forward`` (field_only_v4_chunked_triton_wiki100.py:306-309): the mean of
+    squares over the last dimension, eps added inside the root, then the weight."""
+    x = _f64(x)
+    w = _f64(weight)
+    if w.shape != x.shape[-1:]:
+        raise ValueError(f"weight must be [{x.shape[-1]}], got {w.shape}")
+    ms = np.mean(x * x, axis=-1, keepdims=True)
+    return x / np.sqrt(ms + eps) * w
 
 
 def rel_err(actual, expected) -> float:

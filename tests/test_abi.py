@@ -34,7 +34,8 @@ def lib():
 def test_header_declares_expected_entry_points():
     names = _declared_functions()
     assert {"fl_scan_forward", "fl_scan_forward_ex", "fl_scan_workspace_bytes",
-            "fl_decode_step", "fl_version"} <= set(names)
+            "fl_scan_norm_forward", "fl_decode_step", "fl_decode_norm_step",
+            "fl_version"} <= set(names)
 
 
 def test_library_exports_every_declared_symbol(lib):
@@ -93,6 +94,36 @@ def test_argument_validation_returns_before_launch(lib):
     assert lib.fl_decode_step(16, 0, 0, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
     assert lib.fl_decode_step(16, 0, 1, 8, 23, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
     assert lib.fl_decode_step(None, 0, 1, 8, 24, 16, 16, 16, 16, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+
+
+def _scan_norm(lib, **kw):
+    a = dict(raw=256, raw_dtype=0, B=1, T=4, C=8, sb=4 * 24, st=24, tr=256, ti=256, gamma=256,
+             state_in=None, state_out=None, w=256, eps=1e-6, out=256, out_dtype=0, ws=256,
+             ws_bytes=1 << 40, stream=None)
+    a.update(kw)
+    return lib.fl_scan_norm_forward(a["raw"], a["raw_dtype"], a["B"], a["T"], a["C"], a["sb"], a["st"],
+                                    a["tr"], a["ti"], a["gamma"], a["state_in"], a["state_out"],
+                                    a["w"], a["eps"], a["out"], a["out_dtype"], a["ws"],
+                                    a["ws_bytes"], a["stream"])
+
+
+def test_norm_argument_validation_returns_before_launch(lib):
+    assert _scan_norm(lib, w=None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan_norm(lib, w=258) == nat.FL_ERR_INVALID_ARGUMENT  # misaligned weight
+    assert _scan_norm(lib, eps=-1.0) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan_norm(lib, eps=float("nan")) == nat.FL_ERR_INVALID_ARGUMENT
+    assert _scan_norm(lib, out_dtype=7) == nat.FL_ERR_DTYPE
+    assert _scan_norm(lib, ws_bytes=10) == nat.FL_ERR_WORKSPACE
+    # 65 channel tiles of 64: above the cap of tiles resident together
+    assert _scan_norm(lib, C=4160, st=3 * 4160, sb=4 * 3 * 4160) == nat.FL_ERR_INVALID_ARGUMENT
+    dn = lib.fl_decode_norm_step
+    assert dn(16, 0, 1, 8, 24, 16, 16, 16, 16, 16, 1e-6, 16, 7, None) == nat.FL_ERR_DTYPE
+    assert dn(16, 5, 1, 8, 24, 16, 16, 16, 16, 16, 1e-6, 16, 0, None) == nat.FL_ERR_DTYPE
+    assert dn(16, 0, 0, 8, 24, 16, 16, 16, 16, 16, 1e-6, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert dn(16, 0, 1, 8, 23, 16, 16, 16, 16, 16, 1e-6, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert dn(16, 0, 1, 8, 24, 16, 16, 16, 16, None, 1e-6, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert dn(16, 0, 1, 8, 24, 16, 16, 16, 16, 16, -1.0, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert dn(16, 0, 1, 8, 24, 16, 16, 16, 16, 18, 1e-6, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
 
 
 def test_error_mapping():

@@ -1,0 +1,323 @@
+"""GPU parity of the scan / decode step with the read_norm RMSNorm fused into the epilogue
+(fl_scan_norm_forward, fl_decode_norm_step) against the float64 oracle.
+
+Tolerances: norm-wise relative error <= 1e-4 for fp32 output (the bar of the scan itself);
+bf16 output must equal the fp32 output rounded to nearest even, bit for bit; the fused and
+unfused module paths agree to 1e-5 (fp32) since they differ only in summation order.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from fields_lm_amd import _native
+
+    _native.load()
+    return torch.device("cuda:0")
+
+
+def _params(C, seed):
+    rl, th = ref.init_radius_theta(C)
+    g = torch.Generator().manual_seed(seed)
+    rl = rl + 0.5 * torch.randn(C, generator=g)
+    th = th + 0.3 * torch.randn(C, generator=g)
+    return ref.transition_params(rl, th)
+
+
+def _weight(C, seed):
+    g = torch.Generator().manual_seed(seed + 17)
+    return 1.0 + 0.5 * torch.randn(4 * C, generator=g)
+
+
+def _to(dev, *ts):
+    return [t.to(dev).contiguous() for t in ts]
+
+
+# C = 48, 6, 5: one partial channel tile; 512: 8 tiles; 1024: 16; 4096: 64 (the maximum)
+SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
+          (4, 257, 512), (2, 1000, 1024), (1, 300, 4096)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_scan_norm_matches_oracle(dev, shape, dtype):
+    from fields_lm_amd import field_scan_norm
+
+    B, T, C = shape
+    print(f"[case] scan_norm shape={shape} dtype={dtype}", flush=True)
+    g = torch.Generator().manual_seed(B * 1000 + T + C)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+    sin = torch.randn(B, 2 * C, generator=g) * 0.3
+    tr, ti, gamma = _params(C, seed=C)
+    w = _weight(C, C)
+    for eps in (1e-6, 0.05):
+        out, state = field_scan_norm(*_to(dev, raw, tr, ti, gamma, w), eps=eps,
+                                     state_in=sin.to(dev), return_state=True)
+        torch.cuda.synchronize()
+        exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
+        exp = oracle.rms_norm_f64(exp_read, w, eps)
+        assert out.dtype == torch.float32
+        assert oracle.rel_err(out.cpu(), exp) <= TOL, eps
+        assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+        # every row is normalised on its own: check the worst row too
+        got = out.cpu().double().numpy()
+        row_err = abs(got - exp).max(axis=-1) / abs(exp).max(axis=-1).clip(1e-30)
+        assert float(row_err.max()) <= 1e-3, float(row_err.max())
+
+
+def test_norm_bf16_out_is_rounded_fp32_out(dev):
+    """bf16 output = fp32 output rounded to nearest even; state_out equals the plain scan's."""
+    from fields_lm_amd import field_scan, field_scan_norm
+
+    print("[case] scan_norm bf16 out", flush=True)
+    for (B, T, C, dtype) in [(2, 37, 32, torch.float32), (3, 1000, 512, torch.bfloat16),
+                             (2, 130, 7, torch.bfloat16), (1, 4099, 64, torch.float32)]:
+        g = torch.Generator().manual_seed(B + T + C)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+        sin = torch.randn(B, 2 * C, generator=g) * 0.2
+        draw, tr, ti, gamma, w = _to(dev, raw, *_params(C, seed=C), _weight(C, C))
+        o32, s32 = field_scan_norm(draw, tr, ti, gamma, w, state_in=sin.to(dev), return_state=True)
+        o16, s16 = field_scan_norm(draw, tr, ti, gamma, w, state_in=sin.to(dev), return_state=True,
+                                   out_dtype=torch.bfloat16)
+        _, s_plain = field_scan(draw, tr, ti, gamma, state_in=sin.to(dev), return_state=True)
+        assert o16.dtype == torch.bfloat16
+        torch.testing.assert_close(o16, o32.to(torch.bfloat16), rtol=0, atol=0)
+        torch.testing.assert_close(s16, s32, rtol=0, atol=0)
+        torch.testing.assert_close(s32, s_plain, rtol=0, atol=0)
+
+
+def test_norm_equals_rmsnorm_module_of_read(dev):
+    """Fused epilogue == the package's RMSNorm module applied to the plain scan's fp32 read."""
+    from fields_lm_amd import RMSNorm, field_scan, field_scan_norm
+
+    print("[case] scan_norm vs RMSNorm(read)", flush=True)
+    B, T, C = 3, 777, 512
+    g = torch.Generator().manual_seed(9)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+    draw, tr, ti, gamma, w = _to(dev, raw, *_params(C, seed=9), _weight(C, 9))
+    norm = RMSNorm(4 * C).to(dev)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+        expect = norm(field_scan(draw, tr, ti, gamma))
+    got = field_scan_norm(draw, tr, ti, gamma, w)
+    assert oracle.rel_err(got.cpu(), expect.cpu()) <= 1e-5
+
+
+def test_norm_state_continuation(dev):
+    from fields_lm_amd import field_scan_norm
+
+    print("[case] scan_norm continuation", flush=True)
+    B, T, C, cut = 2, 700, 256, 333
+    g = torch.Generator().manual_seed(11)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+    draw, tr, ti, gamma, w = _to(dev, raw, *_params(C, seed=11), _weight(C, 11))
+    full, s_full = field_scan_norm(draw, tr, ti, gamma, w, return_state=True)
+    a, s_a = field_scan_norm(draw[:, :cut], tr, ti, gamma, w, return_state=True)
+    b, s_b = field_scan_norm(draw[:, cut:], tr, ti, gamma, w, state_in=s_a, return_state=True)
+    assert oracle.rel_err(torch.cat([a, b], 1).cpu(), full.cpu()) <= TOL
+    assert oracle.rel_err(s_b.cpu(), s_full.cpu()) <= TOL
+
+
+def test_norm_and_plain_calls_share_a_workspace(dev):
+    """Plain and fused launches alternate on one workspace (one stream) without interference."""
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd import _native as nat
+
+    print("[case] scan_norm workspace sharing", flush=True)
+    B, T, C = 2, 900, 512
+    g = torch.Generator().manual_seed(12)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+    tr, ti, gamma = _params(C, seed=12)
+    w = _weight(C, 12)
+    draw, dtr, dti, dgm, dw = _to(dev, raw, tr, ti, gamma, w)
+    plain = ScanPlan(draw, dtr, dti, dgm)
+    fused = ScanPlan(draw, dtr, dti, dgm, norm_weight=dw)
+    fused.workspace = plain.workspace  # same bytes, same size
+    fused.args = fused.args[:-2] + (nat.ptr(plain.workspace), plain.ws_bytes)
+    exp_read, _ = oracle.scan_f64(raw.float(), tr, ti, gamma)
+    exp_norm = oracle.rms_norm_f64(exp_read, w, 1e-6)
+    for _ in range(3):
+        plain.run()
+        fused.run()
+        torch.cuda.synchronize()
+        assert oracle.rel_err(plain.read.cpu(), exp_read) <= TOL
+        assert oracle.rel_err(fused.read.cpu(), exp_norm) <= TOL
+    assert nat.workspace_error(plain.workspace) == 0
+
+
+def test_norm_plan_graph_replays(dev):
+    from fields_lm_amd import ScanPlan, field_scan_norm
+    from fields_lm_amd import _native as nat
+
+    print("[case] scan_norm graph", flush=True)
+    B, T, C = 2, 600, 512
+    tr, ti, gamma, w = _to(dev, *_params(C, 3), _weight(C, 3))
+    raw = torch.zeros(B, T, 3 * C, device=dev, dtype=torch.bfloat16)
+    plan = ScanPlan(raw, tr, ti, gamma, read_dtype=torch.bfloat16, norm_weight=w)
+    plan.run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.run()
+    g = torch.Generator().manual_seed(3)
+    for _ in range(4):
+        raw.copy_((torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager, state = field_scan_norm(raw, tr, ti, gamma, w, return_state=True,
+                                       out_dtype=torch.bfloat16)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(plan.read, eager, rtol=0, atol=0)
+        torch.testing.assert_close(plan.state_out, state, rtol=0, atol=0)
+    assert nat.workspace_error(plan.workspace) == 0
+
+
+@pytest.mark.parametrize("name", ["scan_b8_t2048_d1024", "scan_b1_t65536_d1024"])
+def test_norm_full_size_workloads(dev, name):
+    """Configs 2 and 4: fused bf16 output against the float64 oracle's normalised read."""
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd.workloads import make_scan_workload
+
+    print(f"[case] scan_norm full size {name}", flush=True)
+    wl = make_scan_workload(name, dev)
+    C = wl.channels
+    w = _weight(C, 4).to(dev)
+    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, read_dtype=torch.bfloat16, norm_weight=w)
+    out = plan.run()
+    torch.cuda.synchronize()
+    assert nat.workspace_error(plan.workspace) == 0
+    exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
+    exp = oracle.rms_norm_f64(exp_read, w.cpu(), 1e-6)
+    del exp_read
+    assert oracle.rel_err(out.float().cpu(), exp) <= 4e-3  # bf16 rounding: 2^-9 relative
+    assert oracle.rel_err(plan.state_out.cpu(), exp_state) <= TOL
+
+
+def test_norm_errors(dev):
+    from fields_lm_amd import field_scan_norm
+
+    print("[case] scan_norm errors", flush=True)
+    C = 4160  # 65 channel tiles: above the resident-group cap
+    raw = torch.zeros(1, 4, 3 * C, device=dev)
+    p = torch.ones(C, device=dev)
+    with pytest.raises(ValueError):
+        field_scan_norm(raw, p, p, p, torch.ones(4 * C, device=dev))
+    raw = torch.zeros(1, 4, 96, device=dev)
+    p = torch.ones(32, device=dev)
+    with pytest.raises(ValueError):
+        field_scan_norm(raw, p, p, p, torch.ones(64, device=dev))  # weight not 4C
+    with pytest.raises(TypeError):
+        field_scan_norm(raw, p, p, p, torch.ones(128, device=dev), out_dtype=torch.float16)
+    with pytest.raises(ValueError):
+        field_scan_norm(raw, p, p, p, torch.ones(128, device=dev), eps=-1.0)
+
+
+# ---------------------------------------------------------------------------------------------
+# decode step with the epilogue
+# ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("C", [32, 5, 512, 1000])
+def test_decode_norm_steps_reproduce_scan_norm(dev, C, dtype):
+    from fields_lm_amd import field_decode_norm_step, field_scan_norm
+
+    B, T = 3, 40
+    print(f"[case] decode_norm C={C} dtype={dtype}", flush=True)
+    g = torch.Generator().manual_seed(C + 5)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+    tr, ti, gamma = _params(C, C)
+    w = _weight(C, C)
+    draw, dtr, dti, dgm, dw = _to(dev, raw, tr, ti, gamma, w)
+    full = field_scan_norm(draw, dtr, dti, dgm, dw)
+    state = torch.zeros(B, 2 * C, device=dev)
+    state16 = torch.zeros(B, 2 * C, device=dev)
+    rows, rows16 = [], []
+    for t in range(T):
+        rows.append(field_decode_norm_step(draw[:, t], dtr, dti, dgm, state, dw))
+        rows16.append(field_decode_norm_step(draw[:, t], dtr, dti, dgm, state16, dw,
+                                             out_dtype=torch.bfloat16))
+    steps = torch.stack(rows, 1)
+    exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma)
+    assert oracle.rel_err(steps.cpu(), oracle.rms_norm_f64(exp_read, w, 1e-6)) <= TOL
+    assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+    assert oracle.rel_err(steps.cpu(), full.cpu()) <= TOL
+    torch.testing.assert_close(torch.stack(rows16, 1), steps.to(torch.bfloat16), rtol=0, atol=0)
+    torch.testing.assert_close(state16, state, rtol=0, atol=0)
+
+
+def test_decode_norm_b64_against_oracle(dev):
+    from fields_lm_amd import field_decode_norm_step
+
+    B, C = 64, 512
+    print("[case] decode_norm B64", flush=True)
+    g = torch.Generator().manual_seed(64)
+    raw_t = torch.randn(B, 3 * C, generator=g).to(torch.bfloat16)
+    state = torch.randn(B, 2 * C, generator=g) * 0.5
+    tr, ti, gamma = _params(C, 64)
+    w = _weight(C, 64)
+    dstate = state.to(dev)
+    out = field_decode_norm_step(*_to(dev, raw_t, tr, ti, gamma), dstate, w.to(dev), 1e-6)
+    exp_out, exp_state = oracle.decode_step_f64(raw_t.float(), tr, ti, gamma, state)
+    assert oracle.rel_err(out.cpu(), oracle.rms_norm_f64(exp_out, w, 1e-6)) <= TOL
+    assert oracle.rel_err(dstate.cpu(), exp_state) <= TOL
+
+
+# ---------------------------------------------------------------------------------------------
+# module paths
+# ---------------------------------------------------------------------------------------------
+
+def test_module_fused_equals_unfused(dev):
+    from fields_lm_amd import FieldBlock
+
+    print("[case] module fused vs unfused", flush=True)
+    torch.manual_seed(21)
+    block = FieldBlock(512, "triton", 32, 32, 64, 1024).to(dev)
+    with torch.no_grad():
+        block.mixer.read_norm.weight.copy_(_weight(256, 21))
+    x = torch.randn(2, 300, 512, device=dev)
+    with torch.no_grad():
+        block.mixer.fuse_read_norm = False
+        ref_out = block(x)
+        y_ref, s_ref = block.prefill(x[:, :200])
+        _, s_end_ref = block.prefill(x)
+        block.mixer.fuse_read_norm = True
+        out = block(x)
+        y, s = block.prefill(x[:, :200])
+        s_200 = s.clone()
+        params = block.mixer.transition()
+        steps = [block.step(x[:, t], s, params) for t in range(200, 300)]  # advances s in place
+    assert oracle.rel_err(out.cpu(), ref_out.cpu()) <= 1e-5
+    assert oracle.rel_err(y.cpu(), y_ref.cpu()) <= 1e-5
+    torch.testing.assert_close(s_200, s_ref, rtol=0, atol=0)  # same recurrence, same rounding
+    assert oracle.rel_err(s.cpu(), s_end_ref.cpu()) <= 1e-4
+    assert oracle.rel_err(torch.stack(steps, 1).cpu(), ref_out[:, 200:].cpu()) <= 1e-4
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        block.mixer.fuse_read_norm = False
+        ref16 = block(x)
+        block.mixer.fuse_read_norm = True
+        out16 = block(x)
+    assert oracle.rel_err(out16.float().cpu(), ref16.float().cpu()) <= 2e-2
+
+
+def test_module_fused_forward_is_forward_only(dev):
+    from fields_lm_amd import IndependentVacancyField
+
+    print("[case] module fused backward raises", flush=True)
+    mixer = IndependentVacancyField(64, "triton", 32, 32, 64).to(dev)
+    x = torch.randn(1, 10, 64, device=dev, requires_grad=True)
+    y = mixer(x)
+    with pytest.raises(NotImplementedError):
+        y.sum().backward()

@@ -352,14 +352,19 @@ def test_block_fp32_matches_reference_golden(dev, golden_dir):
     block = block.to(dev)
     rec = {}
     h = block.mixer.read_norm.register_forward_pre_hook(lambda m, i: rec.__setitem__("read", i[0].detach()))
+    block.mixer.fuse_read_norm = False  # read_norm as a separate module call: read is visible
     with torch.no_grad():
         out = block(torch.from_numpy(d["x"]).to(dev))
     h.remove()
     assert oracle.rel_err(rec["read"].cpu(), d["read"]) <= TOL
     assert oracle.rel_err(out.cpu(), d["block_out"]) <= TOL
-    with torch.no_grad():
-        mix = block.mixer(torch.from_numpy(d["x"]).to(dev))
-    assert oracle.rel_err(mix.cpu(), d["mixer_out"]) <= TOL
+    for fused in (False, True):
+        block.mixer.fuse_read_norm = fused
+        with torch.no_grad():
+            mix = block.mixer(torch.from_numpy(d["x"]).to(dev))
+            out = block(torch.from_numpy(d["x"]).to(dev))
+        assert oracle.rel_err(mix.cpu(), d["mixer_out"]) <= TOL, fused
+        assert oracle.rel_err(out.cpu(), d["block_out"]) <= TOL, fused
 
 
 def test_block_bf16_autocast_matches_reference_golden(dev, golden_dir):

@@ -89,6 +89,46 @@ def test_golden_config1_rows(golden_dir):
     assert oracle.rel_err(s64[0], d["final_state"].reshape(-1)) <= 1e-5
 
 
+def _mixer_out_from_read(sd, x, normed):
+    """x + out_proj(normed) * sigmoid(gate_proj(x)) in float64 from the golden parameters."""
+    x = x.astype(np.float64)
+    w = lambda k: sd["mixer." + k].double().numpy()  # noqa: E731
+    out = normed @ w("out_proj.weight").T + w("out_proj.bias")
+    gate = 1.0 / (1.0 + np.exp(-(x @ w("gate_proj.weight").T + w("gate_proj.bias"))))
+    return x + out * gate
+
+
+def test_golden_rms_norm_of_read(golden_dir):
+    """rms_norm_f64 applied to the reference's read reproduces the reference's mixer output
+    (its read_norm sits between them, eps 1e-6, canon:1193); mean over 2C instead of 4C, or eps
+    outside the root, miss it."""
+    d = np.load(golden_dir / "selftest_block.npz")
+    sd = {k[len("param::"):]: torch.from_numpy(d[k]) for k in d.files if k.startswith("param::")}
+    w = sd["mixer.read_norm.weight"]
+    normed = oracle.rms_norm_f64(d["read"], w, 1e-6)
+    assert oracle.rel_err(_mixer_out_from_read(sd, d["x"], normed), d["mixer_out"]) <= 1e-5
+    r = d["read"].astype(np.float64)
+    half = r / np.sqrt(np.mean(r[..., : r.shape[-1] // 2] ** 2, axis=-1, keepdims=True) + 1e-6)
+    assert oracle.rel_err(_mixer_out_from_read(sd, d["x"], half), d["mixer_out"]) > 1e-3
+    r = d["read"][:, :3].astype(np.float64) * 1e-3  # tiny rows: eps inside vs outside the root
+    inside = oracle.rms_norm_f64(r, np.ones(r.shape[-1]), 1e-6)
+    outside = r / (np.sqrt(np.mean(r * r, axis=-1, keepdims=True)) + 1e-6)
+    assert oracle.rel_err(outside, inside) > 1e-4
+
+
+def test_rms_norm_invariants():
+    """Unit RMS with unit weight and eps 0; scale invariance; weight acts per column; eps -> big
+    gives x / sqrt(eps)."""
+    g = np.random.default_rng(5)
+    x = g.standard_normal((3, 7, 64)) * g.uniform(0.1, 10, (3, 7, 1))
+    y = oracle.rms_norm_f64(x, np.ones(64), 0.0)
+    np.testing.assert_allclose(np.sqrt(np.mean(y * y, axis=-1)), 1.0, rtol=1e-12)
+    np.testing.assert_allclose(oracle.rms_norm_f64(x * 37.0, np.ones(64), 0.0), y, rtol=1e-12)
+    w = g.standard_normal(64)
+    np.testing.assert_allclose(oracle.rms_norm_f64(x, w, 0.0), y * w, rtol=1e-12)
+    np.testing.assert_allclose(oracle.rms_norm_f64(x, np.ones(64), 1e12), x / 1e6, rtol=1e-9)
+
+
 # ---------------------------------------------------------------------------------------------
 # closed forms
 # ---------------------------------------------------------------------------------------------
