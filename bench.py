@@ -8,7 +8,11 @@ MI355X's 8 TB/s HBM with the algorithmic bytes 3C*2 + 4C*4 = 11,264 B/token; ``c
 times the torch restatement of the reference's CPU path (oracle/reference_path.py) on the
 host's cores on the same workload.
 
-    python bench.py [--steps K] [--warmup W] [--workload NAME] [--no-cpu-baseline] [--no-extras]
+    python bench.py [--steps K] [--warmup W] [--workload NAME] [--variant V] [--no-cpu-baseline]
+                    [--no-extras] [--decode-only]
+
+``--variant`` picks the timed scan: read_fp32 (the headline: fp32 read, 11,264 B/token),
+read_bf16 (7,168 B/token), norm_bf16 / norm_fp32 (read_norm fused into the epilogue).
 """
 from __future__ import annotations
 
@@ -48,9 +52,17 @@ def copy_calibration() -> int:
     return 0
 
 
-def measured_traffic(workload: str):
+VARIANTS = {  # name -> (ScanPlan keyword arguments, read bytes per element, profile suffix)
+    "read_fp32": ({}, 4, ""),
+    "read_bf16": ({"read_dtype": "bf16"}, 2, "_read_bf16"),
+    "norm_bf16": ({"read_dtype": "bf16", "norm": True}, 2, "_norm_bf16"),
+    "norm_fp32": ({"norm": True}, 4, "_norm_fp32"),
+}
+
+
+def measured_traffic(workload: str, variant: str = "read_fp32"):
     """HBM bytes per launch of the scan from the committed rocprofv3 --pmc summary, or None."""
-    path = REPO / "profiles" / f"fl_scan_lookback_kernel_{workload}_pmc.txt"
+    path = REPO / "profiles" / f"fl_scan_lookback_kernel_{workload}{VARIANTS[variant][2]}_pmc.txt"
     if not path.exists():
         return None
     vals = {}
@@ -120,54 +132,164 @@ def cpu_baseline(workload_name: str, runs: int = 5):
     }
 
 
-def decode_timing(batch: int = 64, dim: int = 1024, tokens: int = 256):
-    """Fused decode step of one Field block at B=64: per-step device time inside a HIP graph of
-    ``tokens`` consecutive steps, and eager single-step latency."""
+def _graph_us_per_call(fn_list, reps: int = 5) -> float:
+    """Capture the calls of ``fn_list`` in one HIP graph; device time per call over ``reps`` replays."""
     import torch
 
-    from fields_lm_amd import field_decode_step
-    from fields_lm_amd.workloads import make_scan_workload
-
-    wl = make_scan_workload("scan_b8_t2048_d1024", "cuda", batch=batch, length=tokens)
-    raw = wl.raw  # [B, tokens, 3C] bf16
-    C = wl.channels
-    state = torch.zeros(batch, 2 * C, device="cuda")
-    out = torch.empty(tokens, batch, 4 * C, device="cuda")
-    steps = [raw[:, t] for t in range(tokens)]
-    for t in range(4):
-        field_decode_step(steps[t], wl.tr, wl.ti, wl.gamma, state, out=out[t])
+    for fn in fn_list[:2]:
+        fn()
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for t in range(tokens):
-            field_decode_step(steps[t], wl.tr, wl.ti, wl.gamma, state, out=out[t])
+        for fn in fn_list:
+            fn()
     torch.cuda.synchronize()
     graph.replay()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    reps = 5
     start.record()
     for _ in range(reps):
         graph.replay()
     end.record()
     torch.cuda.synchronize()
-    graph_us = start.elapsed_time(end) * 1e3 / (reps * tokens)
+    return start.elapsed_time(end) * 1e3 / (reps * len(fn_list))
+
+
+def _eager_p50_us(fn, n: int = 64) -> float:
+    import torch
+
     lat = []
-    for t in range(64):
+    for _ in range(n):
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        field_decode_step(steps[t], wl.tr, wl.ti, wl.gamma, state, out=out[t])
+        fn()
         torch.cuda.synchronize()
         lat.append((time.perf_counter() - t0) * 1e6)
-    bytes_step = batch * (3 * C * 2 + 2 * C * 4 * 2 + 4 * C * 4)
+    return statistics.median(lat)
+
+
+def _torch_step(raw_t, lam, gamma, s):
+    """Stock-PyTorch eager single-token Field step (complex64), the comparator for the fused
+    kernel: the gates and update of the reference's recurrence for one token."""
+    import torch
+
+    c = lam.numel()
+    zr, zi, zv = raw_t.float().split(c, dim=-1)
+    inj = torch.complex(torch.tanh(zr), torch.tanh(zi))
+    v = 0.9 * torch.sigmoid(zv)
+    m = lam * s
+    disp = v * m
+    s_new = (1.0 - v) * m + gamma * v * inj
+    return torch.cat([s_new.real, s_new.imag, disp.real, disp.imag], -1), s_new
+
+
+def decode_comparison(batch: int = 64, dim: int = 1024, prompt: int = 2048, tokens: int = 256):
+    """Decode at B=64 (config 5's per-token Field work), one Field block:
+
+    * kernel: fl_decode_norm_step (state update + displaced readout + read_norm, one launch)
+      and fl_decode_step, per step inside a HIP graph of ``tokens`` consecutive steps;
+    * block_step: the whole FieldBlock.step (projections, fused step, gate, SwiGLU), bf16
+      weights, per token inside a HIP graph of 32 tokens, and eager p50;
+    * reference procedure: the reference has no incremental state, so token t's Field output
+      needs the block re-run over the whole prefix (length prompt + t >= prompt): timed as one
+      FieldBlock.forward over [B, prompt] with this package's kernels (a lower bound of the
+      reference's per-token cost);
+    * torch_eager_step: a stock-PyTorch eager single-token step (complex64 ops), p50.
+    """
+    import torch
+
+    from fields_lm_amd import FieldBlock, field_decode_norm_step, field_decode_step
+    from fields_lm_amd.workloads import make_scan_workload
+
+    dev = torch.device("cuda:0")
+    wl = make_scan_workload("scan_b8_t2048_d1024", dev, batch=batch, length=tokens)
+    raw = wl.raw  # [B, tokens, 3C] bf16
+    C = wl.channels
+    w = torch.ones(4 * C, device=dev)
+    state = torch.zeros(batch, 2 * C, device=dev)
+    out32 = torch.empty(tokens, batch, 4 * C, device=dev)
+    out16 = torch.empty(tokens, batch, 4 * C, device=dev, dtype=torch.bfloat16)
+    steps = [raw[:, t] for t in range(tokens)]
+    plain_us = _graph_us_per_call(
+        [lambda t=t: field_decode_step(steps[t], wl.tr, wl.ti, wl.gamma, state, out=out32[t])
+         for t in range(tokens)])
+    norm_us = _graph_us_per_call(
+        [lambda t=t: field_decode_norm_step(steps[t], wl.tr, wl.ti, wl.gamma, state, w,
+                                            out=out16[t], out_dtype=torch.bfloat16)
+         for t in range(tokens)])
+    kernel_p50 = _eager_p50_us(lambda: field_decode_norm_step(steps[0], wl.tr, wl.ti, wl.gamma, state, w,
+                                                              out=out16[0], out_dtype=torch.bfloat16))
+    lam = torch.complex(wl.tr, wl.ti)
+    s_c = torch.zeros(batch, C, device=dev, dtype=torch.complex64)
+    torch_p50 = _eager_p50_us(lambda: _torch_step(steps[0], lam, wl.gamma, s_c))
+    del out32, out16
+
+    torch.manual_seed(5)
+    block = FieldBlock(dim, "triton", 32, 32, 64, 2752).to(device=dev, dtype=torch.bfloat16)
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(batch, prompt, dim, device=dev, dtype=torch.bfloat16, generator=g)
+    xt = torch.randn(32, batch, dim, device=dev, dtype=torch.bfloat16, generator=g)
+    with torch.no_grad():
+        _, bstate = block.prefill(x)
+        params = block.mixer.transition()
+        block_us = _graph_us_per_call([lambda t=t: block.step(xt[t], bstate, params) for t in range(32)])
+        block_p50 = _eager_p50_us(lambda: block.step(xt[0], bstate, params), n=32)
+        reforward = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            block(x)
+            torch.cuda.synchronize()
+            reforward.append((time.perf_counter() - t0) * 1e6)
+    ref_us = statistics.median(reforward)
+    del x, block
+    torch.cuda.empty_cache()
+    bytes_step = batch * (3 * C * 2 + 2 * C * 4 * 2 + 4 * C * 2)
     return {
         "batch": batch,
-        "graph_us_per_step": graph_us,
-        "graph_tokens_per_s": batch / (graph_us * 1e-6),
-        "eager_p50_us": statistics.median(lat),
-        "bytes_per_step": bytes_step,
-        "graph_gbs": bytes_step / (graph_us * 1e-6) / 1e9,
+        "kernel_norm_graph_us_per_step": norm_us,
+        "kernel_norm_eager_p50_us": kernel_p50,
+        "kernel_norm_bytes_per_step": bytes_step,
+        "kernel_norm_graph_gbs": bytes_step / (norm_us * 1e-6) / 1e9,
+        "kernel_plain_graph_us_per_step": plain_us,
+        "block_step_graph_us_per_token": block_us,
+        "block_step_graph_tokens_per_s": batch / (block_us * 1e-6),
+        "block_step_eager_p50_us": block_p50,
+        "reference_procedure_prefix_reforward_us": ref_us,
+        "reference_procedure_prefix": prompt,
+        "torch_eager_step_p50_us": torch_p50,
+        "speedup_block_step_vs_reference_procedure": ref_us / block_us,
+        "note": "block: FieldBlock(1024, ff_hidden 2752) bf16 weights, random init seed 5; "
+                "reference procedure = full-prefix re-forward per token (prefix >= 2048), run "
+                "with this package's kernels, so it is a lower bound of the reference's cost",
     }
+
+
+def cpu_decode_reforward(runs: int = 3):
+    """Reference CPU path per-token cost of decode: one full-prefix re-forward of the Field block
+    (oracle/reference_path.py, the reference's CPU path restated) at B=1, T=2048, fp32."""
+    import torch
+
+    import oracle  # noqa: F401  (checker package; timed CPU baseline only)
+    from oracle import reference_path as ref
+    from fields_lm_amd import FieldBlock
+
+    torch.manual_seed(0)
+    block = FieldBlock(1024, "triton", 32, 32, 64, 2752)
+    sd = {k: v.detach() for k, v in block.state_dict().items()}
+    x = torch.randn(1, 2048, 1024)
+    with torch.no_grad():
+        ref.block_forward(sd, x, field_chunk=32)
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            ref.block_forward(sd, x, field_chunk=32)
+            times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {"us_per_token_b1": med * 1e6, "batch": 1, "prefix": 2048, "dtype": "fp32",
+            "cores": len(os.sched_getaffinity(0)),
+            "sample": f"FieldBlock(1024, ff_hidden 2752) seed 0, x ~ N(0,1) [1,2048,1024]; "
+                      f"median of {runs} after 1 warm-up; at B=64 the re-forward is ~64x this"}
 
 
 def main() -> int:
@@ -176,6 +298,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="scan_b8_t2048_d1024")
+    ap.add_argument("--variant", default="read_fp32", choices=list(VARIANTS))
+    ap.add_argument("--decode-only", action="store_true",
+                    help="only the B=64 decode comparison (kernel and block step in HIP graphs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -200,11 +325,20 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     dev = torch.device("cuda:0")
-    log(f"[bench] device={torch.cuda.get_device_name(dev)} workload={args.workload}")
+    if args.decode_only:
+        print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
+        return 0
+    log(f"[bench] device={torch.cuda.get_device_name(dev)} workload={args.workload} variant={args.variant}")
     wl = make_scan_workload(args.workload, dev)
-    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma)
+    vkw, read_bytes, _ = VARIANTS[args.variant]
+    kw = {}
+    if vkw.get("read_dtype") == "bf16":
+        kw["read_dtype"] = torch.bfloat16
+    if vkw.get("norm"):
+        kw["norm_weight"] = torch.ones(4 * wl.channels, device=dev)  # read_norm's init weight
+    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
     wall_ms, ev_ms = time_plan(plan, args.steps, args.warmup)
-    bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype)
+    bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype, read_bytes)
     alg_bytes = bpt * wl.tokens
     achieved = alg_bytes / (ev_ms * 1e-3) / 1e9
     log(f"[bench] {args.workload}: wall {wall_ms * 1e3:.1f} us/step, events {ev_ms * 1e3:.1f} us/step, "
@@ -224,9 +358,10 @@ def main() -> int:
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": args.workload,
+            "workload": args.workload, "variant": args.variant,
             "B": wl.raw.shape[0], "T": wl.raw.shape[1], "d_model": 2 * wl.channels,
-            "raw_dtype": "bf16", "read_dtype": "fp32", "state_dtype": "fp32",
+            "raw_dtype": "bf16", "read_dtype": "fp32" if read_bytes == 4 else "bf16",
+            "state_dtype": "fp32", "read_norm_fused": bool(vkw.get("norm")),
             "bytes_per_token": bpt, "parallelism": "single-gpu",
         },
         "roofline": {
@@ -236,7 +371,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(args.workload),
+            "traffic": measured_traffic(args.workload, args.variant),
             "algorithmic_bytes": alg_bytes,
             "event_us_per_launch": ev_ms * 1e3,
         },
@@ -265,12 +400,47 @@ def main() -> int:
                                             "frac_hbm_peak": bl / (el * 1e-3) / 1e9 / HBM_PEAK_GBS}
         del pl, wll
         torch.cuda.empty_cache()
-        extras["decode_b64_one_block"] = decode_timing()
+        # bf16 read, fused read_norm (bf16 / fp32 out), and the unfused sequence it replaces
+        wl = make_scan_workload(args.workload, dev)
+        C = wl.channels
+        w = torch.ones(4 * C, device=dev)
+        for key, kw, read_bytes in [("bf16_read", dict(read_dtype=torch.bfloat16), 2),
+                                    ("fused_read_norm_bf16_out", dict(read_dtype=torch.bfloat16, norm_weight=w), 2),
+                                    ("fused_read_norm_fp32_out", dict(norm_weight=w), 4)]:
+            pp = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
+            _, e = time_plan(pp, 100, 10)
+            nb = scan_bytes_per_token(C, wl.raw.dtype, read_bytes) * wl.tokens
+            extras[key] = {"us_per_step": e * 1e3, "tokens_per_s": wl.tokens / (e * 1e-3),
+                           "bytes_per_token": nb // wl.tokens, "gbs": nb / (e * 1e-3) / 1e9,
+                           "frac_hbm_peak": nb / (e * 1e-3) / 1e9 / HBM_PEAK_GBS}
+            del pp
+        from fields_lm_amd import RMSNorm
+
+        norm = RMSNorm(4 * C).to(dev)
+        pp = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma)
+
+        class _Unfused:
+            device = dev
+
+            def run(self, stream=None):
+                pp.run(stream)
+                with torch.no_grad():
+                    return norm(pp.read).to(torch.bfloat16)
+
+        _, e = time_plan(_Unfused(), 50, 5)
+        extras["unfused_scan_rmsnorm_cast"] = {"us_per_step": e * 1e3,
+                                               "note": "fp32 read, then RMSNorm module, then bf16 cast"}
+        del pp, wl, norm
+        torch.cuda.empty_cache()
+        extras["decode_b64"] = decode_comparison()
         result["extras"] = extras
 
     if not args.no_cpu_baseline:
         log("[bench] cpu baseline ...")
         result["cpu_baseline"] = cpu_baseline(args.workload)
+        if not args.no_extras:
+            log("[bench] cpu decode re-forward ...")
+            result["cpu_baseline"]["decode_reforward"] = cpu_decode_reforward()
 
     print(json.dumps(result), flush=True)
     return 0

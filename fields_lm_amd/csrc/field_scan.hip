@@ -1127,9 +1127,11 @@ __global__ __launch_bounds__(256) void fl_decode_step_kernel(
 }
 
 // Decode step with the RMSNorm epilogue: one block per batch row. Pass 1 forms the row's sum of
-// squares of the four read values over all C channels (state untouched); pass 2 recomputes
-// the step, updates the state in place and stores (value * rsqrt(mean + eps)) * weight. Each
-// channel is owned by one thread in both passes, so the in-place update cannot race.
+// squares of the four read values over all C channels; pass 2 updates the state in place and
+// stores (value * rsqrt(mean + eps)) * weight. With NPER > 0 (C <= 256 * NPER) each thread
+// keeps its NPER channels' values in registers between the passes; with NPER = 0 pass 2
+// recomputes them (any C). Each channel is owned by one thread in both passes, so the in-place
+// update cannot race.
 constexpr int kDecodeNormThreads = 256;
 
 __device__ __forceinline__ void decode_one(float zr, float zi, float zv, float lr, float li,
@@ -1147,7 +1149,7 @@ __device__ __forceinline__ void decode_one(float zr, float zi, float zv, float l
 __device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
 __device__ __forceinline__ void store_out(bf16_bits* p, float v) { *p = (bf16_bits)bf16_bits_of(v); }
 
-template <typename RawT, typename OutT>
+template <typename RawT, typename OutT, int NPER>
 __global__ __launch_bounds__(kDecodeNormThreads) void fl_decode_norm_kernel(
     const RawT* __restrict__ raw_t, int64_t sb, int C, const float* __restrict__ tr,
     const float* __restrict__ ti, const float* __restrict__ gamma, float* __restrict__ state,
@@ -1156,7 +1158,50 @@ __global__ __launch_bounds__(kDecodeNormThreads) void fl_decode_norm_kernel(
   const int b = blockIdx.x;
   const RawT* p = raw_t + (int64_t)b * sb;
   float* s = state + (int64_t)b * 2 * C;
+  OutT* o = out_t + (int64_t)b * 4 * C;
   float acc = 0.f;
+  if constexpr (NPER > 0) {
+    float vr[NPER], vi[NPER], vdr[NPER], vdi[NPER];
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int c = threadIdx.x + i * kDecodeNormThreads;
+      vr[i] = vi[i] = vdr[i] = vdi[i] = 0.f;
+      if (c < C) {
+        float z[3];
+        vr[i] = s[c];
+        vi[i] = s[C + c];
+        Load<RawT, 1>::run(p + c, &z[0]);
+        Load<RawT, 1>::run(p + C + c, &z[1]);
+        Load<RawT, 1>::run(p + 2 * C + c, &z[2]);
+        decode_one(z[0], z[1], z[2], tr[c], ti[c], gamma[c], vr[i], vi[i], vdr[i], vdi[i]);
+        acc = fmaf(vr[i], vr[i], acc);
+        acc = fmaf(vi[i], vi[i], acc);
+        acc = fmaf(vdr[i], vdr[i], acc);
+        acc = fmaf(vdi[i], vdi[i], acc);
+      }
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) acc += __shfl_xor(acc, m);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kDecodeNormThreads / 64; ++w) tot += s_red[w];
+    const float scale = rsqrtf(fmaf(tot, inv_n, eps));
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int c = threadIdx.x + i * kDecodeNormThreads;
+      if (c < C) {
+        s[c] = vr[i];
+        s[C + c] = vi[i];
+        store_out(o + c, (vr[i] * scale) * norm_w[c]);
+        store_out(o + C + c, (vi[i] * scale) * norm_w[C + c]);
+        store_out(o + 2 * C + c, (vdr[i] * scale) * norm_w[2 * C + c]);
+        store_out(o + 3 * C + c, (vdi[i] * scale) * norm_w[3 * C + c]);
+      }
+    }
+    return;
+  }
   for (int c = threadIdx.x; c < C; c += kDecodeNormThreads) {
     float z[3], sr = s[c], si = s[C + c], dr, di;
     Load<RawT, 1>::run(p + c, &z[0]);
@@ -1176,7 +1221,6 @@ __global__ __launch_bounds__(kDecodeNormThreads) void fl_decode_norm_kernel(
 #pragma unroll
   for (int w = 0; w < kDecodeNormThreads / 64; ++w) tot += s_red[w];
   const float scale = rsqrtf(fmaf(tot, inv_n, eps));
-  OutT* o = out_t + (int64_t)b * 4 * C;
   for (int c = threadIdx.x; c < C; c += kDecodeNormThreads) {
     float z[3], sr = s[c], si = s[C + c], dr, di;
     Load<RawT, 1>::run(p + c, &z[0]);
@@ -1576,17 +1620,24 @@ int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
     return FL_ERR_INVALID_ARGUMENT;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float inv_n = (float)(1.0 / (4.0 * (double)C));
-#define FL_DN(R, O)                                                                             \
-  fl_decode_norm_kernel<R, O><<<(unsigned)B, kDecodeNormThreads, 0, s>>>(                        \
+#define FL_DN1(R, O, N)                                                                         \
+  fl_decode_norm_kernel<R, O, N><<<(unsigned)B, kDecodeNormThreads, 0, s>>>(                     \
       static_cast<const R*>(raw_t), raw_stride_b, (int)C, tr, ti, gamma, state, norm_weight, eps, \
       inv_n, static_cast<O*>(out_t));                                                            \
   return hip_status(hipGetLastError());
+#define FL_DN(R, O)                                                                             \
+  if (C <= kDecodeNormThreads) { FL_DN1(R, O, 1) }                                              \
+  if (C <= 2 * kDecodeNormThreads) { FL_DN1(R, O, 2) }                                          \
+  if (C <= 4 * kDecodeNormThreads) { FL_DN1(R, O, 4) }                                          \
+  if (C <= 8 * kDecodeNormThreads) { FL_DN1(R, O, 8) }                                          \
+  FL_DN1(R, O, 0)
   const bool raw16 = raw_dtype == FL_DTYPE_BF16, out16 = out_dtype == FL_DTYPE_BF16;
   if (raw16 && out16) { FL_DN(bf16_bits, bf16_bits) }
   if (raw16) { FL_DN(bf16_bits, float) }
   if (out16) { FL_DN(float, bf16_bits) }
   FL_DN(float, float)
 #undef FL_DN
+#undef FL_DN1
 }
 
 }  // extern "C"

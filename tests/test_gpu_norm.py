@@ -230,7 +230,7 @@ def test_norm_errors(dev):
 # ---------------------------------------------------------------------------------------------
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
-@pytest.mark.parametrize("C", [32, 5, 512, 1000])
+@pytest.mark.parametrize("C", [32, 5, 512, 1000, 1500, 2100])  # register variants 1,1,2,4,8; 2100: recompute
 def test_decode_norm_steps_reproduce_scan_norm(dev, C, dtype):
     from fields_lm_amd import field_decode_norm_step, field_scan_norm
 
