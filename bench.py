@@ -265,6 +265,141 @@ def decode_comparison(batch: int = 64, dim: int = 1024, prompt: int = 2048, toke
     }
 
 
+def _promoted_model(dev):
+    from fields_lm_amd.model import build_official_fields, cast_for_inference
+
+    lm = build_official_fields(device=dev)
+    return lm, cast_for_inference(lm.core_model).eval()
+
+
+def model_prefill(batch: int = 4, length: int = 2048, steps: int = 10, warmup: int = 3):
+    """Config 3: the promoted 18F/2M/4R model (random init, bf16 weights under bf16 autocast)
+    prefilling B=4 x T=2048 uniform tokens (seed 2), logits of the last position as in v32:461-490;
+    whole-model tokens/s, plus per-category device time from events around every block (the
+    breakdown of v32:508-556) and the Field scan kernels' share from their own launch count."""
+    import torch
+
+    from fields_lm_amd.model import _kind
+
+    dev = torch.device("cuda:0")
+    lm, core = _promoted_model(dev)
+    torch.manual_seed(2)
+    tokens = torch.randint(0, 16384, (batch, length)).to(dev)
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        for _ in range(warmup):
+            core.states_logits(tokens, last_only=True)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        start.record()
+        for _ in range(steps):
+            core.states_logits(tokens, last_only=True)
+        end.record()
+        torch.cuda.synchronize()
+        wall_ms = (time.perf_counter() - t0) * 1e3 / steps
+        ev_ms = start.elapsed_time(end) / steps
+        cats = {k: 0.0 for k in ("embedding", "field_blocks", "mamba_blocks", "refresh_blocks",
+                                 "softpatch", "final_norm_head")}
+        reps = 3
+        for _ in range(reps):
+            events = []
+
+            def rec(cat, fn):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                out = fn()
+                b.record()
+                events.append((cat, a, b))
+                return out
+
+            h = rec("embedding", lambda: core.emb(tokens))
+            for i, block in enumerate(core.blocks):
+                cat = {"field": "field_blocks", "mamba": "mamba_blocks", "refresh": "refresh_blocks"}[_kind(block)]
+                h = rec(cat, lambda blk=block, z=h: blk(z))
+                if i == core.patch_position:
+                    h = rec("softpatch", lambda z=h: core.softpatch(z, tokens))
+            rec("final_norm_head", lambda z=h: core.lm_head(core.final_norm(z)[:, -1:]))
+            torch.cuda.synchronize()
+            for cat, a, b in events:
+                cats[cat] += a.elapsed_time(b) / reps
+        # the Field scan kernel alone, one launch per Field block, on a block's real raw
+        fb = next(b for b in core.blocks if _kind(b) == "field")
+        raw = fb.mixer.write_proj(core.emb(tokens))
+        tr, ti, gamma = fb.mixer.transition()
+        from fields_lm_amd import ScanPlan
+
+        plan = ScanPlan(raw.contiguous(), tr, ti, gamma, read_dtype=torch.bfloat16,
+                        norm_weight=fb.mixer.read_norm.weight.float())
+        _, scan_ms = time_plan(plan, 50, 5)
+    total = sum(cats.values())
+    n_field = sum(1 for b in core.blocks if _kind(b) == "field")
+    return {
+        "batch": batch, "length": length, "tokens_per_s": batch * length / (wall_ms * 1e-3),
+        "ms_per_prefill": wall_ms, "event_ms_per_prefill": ev_ms,
+        "category_ms": cats, "category_pct": {k: 100.0 * v / max(total, 1e-9) for k, v in cats.items()},
+        "field_scan_kernel_ms": scan_ms * n_field,
+        "field_scan_kernel_pct": 100.0 * scan_ms * n_field / ev_ms,
+        "params": sum(p.numel() for p in core.parameters()),
+        "ff_hidden": lm.source_audit["ff_hidden"],
+        "note": "random init (model seed 1234), bf16 weights + bf16 autocast; Field blocks run "
+                "read_norm fused into the scan (fl_scan_norm_forward, bf16 out); refresh "
+                "attention, Mamba-2 (PyTorch SSD), projections are stock PyTorch",
+    }
+
+
+def model_decode(batch: int = 64, prompt: int = 2048, new_tokens: int = 256):
+    """Config 5: B=64 streams, a 2,048-token uniform prompt (seed 5), then 256 greedy tokens.
+    Token 1 runs eagerly (warm-up); one decode step plus its argmax feedback is captured in a HIP
+    graph and replayed for every further token, so the loop issues no host work per token."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    lm, core = _promoted_model(dev)
+    torch.manual_seed(5)
+    tokens = torch.randint(0, 16384, (batch, prompt)).to(dev)
+    with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        core.states_logits(tokens[:, :256], last_only=True)  # warm-up of the prefill kernels
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        logits, cache = core.prefill(tokens, max_len=prompt + new_tokens)
+        torch.cuda.synchronize()
+        prefill_ms = (time.perf_counter() - t0) * 1e3
+        tok = logits.argmax(-1)
+        logits = core.step(tok, cache)  # token 1, eager
+        tok.copy_(logits.argmax(-1))
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = core.step(tok, cache)
+            tok.copy_(out.argmax(-1))
+        # tokens 2..new_tokens: one replay each (positions stay below max_len); an event pair
+        # around every replay gives the per-token device latency
+        marks = [torch.cuda.Event(enable_timing=True) for _ in range(new_tokens)]
+        torch.cuda.synchronize()
+        marks[0].record()
+        for i in range(1, new_tokens):
+            graph.replay()
+            marks[i].record()
+        torch.cuda.synchronize()
+        loop_ms = marks[0].elapsed_time(marks[-1])
+        lat = [marks[i - 1].elapsed_time(marks[i]) * 1e3 for i in range(1, new_tokens)]
+        end_pos = int(cache["pos"])
+    if end_pos != prompt + new_tokens:
+        raise RuntimeError(f"decode ended at position {end_pos}, expected {prompt + new_tokens}")
+    per_token_ms = loop_ms / (new_tokens - 1)
+    return {
+        "batch": batch, "prompt": prompt, "new_tokens": new_tokens,
+        "prefill_ms": prefill_ms,
+        "graph_ms_per_token": per_token_ms,
+        "tokens_per_s": batch / (per_token_ms * 1e-3),
+        "p50_token_latency_us": statistics.median(lat),
+        "p90_token_latency_us": sorted(lat)[int(0.9 * (len(lat) - 1))],
+        "reference_procedure_ms_per_token": prefill_ms,
+        "note": "reference procedure = re-running the whole model over the prefix for each new "
+                "token (no incremental state), at least the 2,048-token prefill measured here",
+    }
+
+
 def cpu_decode_reforward(runs: int = 3):
     """Reference CPU path per-token cost of decode: one full-prefix re-forward of the Field block
     (oracle/reference_path.py, the reference's CPU path restated) at B=1, T=2048, fp32."""
@@ -301,6 +436,8 @@ def main() -> int:
     ap.add_argument("--variant", default="read_fp32", choices=list(VARIANTS))
     ap.add_argument("--decode-only", action="store_true",
                     help="only the B=64 decode comparison (kernel and block step in HIP graphs)")
+    ap.add_argument("--model", choices=["prefill", "decode"],
+                    help="only the whole-model run: prefill (config 3) or decode (config 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -327,6 +464,10 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.decode_only:
         print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
+        return 0
+    if args.model:
+        fn = model_prefill if args.model == "prefill" else model_decode
+        print(json.dumps({f"model_{args.model}": fn()}), flush=True)
         return 0
     log(f"[bench] device={torch.cuda.get_device_name(dev)} workload={args.workload} variant={args.variant}")
     wl = make_scan_workload(args.workload, dev)
@@ -433,6 +574,12 @@ def main() -> int:
         del pp, wl, norm
         torch.cuda.empty_cache()
         extras["decode_b64"] = decode_comparison()
+        torch.cuda.empty_cache()
+        log("[bench] model prefill (config 3) ...")
+        extras["model_prefill_b4_t2048"] = model_prefill()
+        torch.cuda.empty_cache()
+        log("[bench] model decode (config 5) ...")
+        extras["model_decode_b64"] = model_decode()
         result["extras"] = extras
 
     if not args.no_cpu_baseline:

@@ -18,12 +18,22 @@ from .field import (  # noqa: F401
     IndependentVacancyField,
     PackedSwiGLU,
     RMSNorm,
+    boundary_scan,
     field_decode_norm_step,
     field_decode_step,
     field_scan,
     field_scan_norm,
     fused_field_read,
     state_to_complex,
+)
+
+from .model import (  # noqa: F401,E402
+    OFFICIAL_ARCHITECTURE,
+    FieldsConfig,
+    FieldsForCausalLM,
+    FieldsForwardOutput,
+    FieldTokenSystem,
+    build_official_fields,
 )
 
 __version__ = "0.1.0"

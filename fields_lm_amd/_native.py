@@ -43,6 +43,7 @@ SIGNATURES = {
     "fl_decode_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _int, _vp]),
     "fl_decode_norm_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                    ctypes.c_float, _vp, _int, _vp]),
+    "fl_boundary_scan": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "fl_version": (ctypes.c_char_p, []),
 }
 

@@ -1237,6 +1237,56 @@ __global__ __launch_bounds__(kDecodeNormThreads) void fl_decode_norm_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
+// Boundary scan of the softpatch (BoundaryStateMixer, v3:441-464 / v6:318-338):
+//   s[b,t,r] = a[b,t] * s[b,t-1,r] + drive[b,t,r],   s[b,-1,:] = state_in or 0,
+// the real-valued first-order recurrence that the reference runs through
+// hierarchical_scan(a, drive, block=32) with a = (1 - boundary) broadcast over the rank.
+// Block = (batch row, 64 channels), W waves; wave w owns steps [w*S, (w+1)*S). Pass 1 forms
+// each wave's map (prod a, state from 0) over its steps, the waves' carries are composed in LDS,
+// pass 2 re-runs from the carry and stores. Lane <-> channel, so each step is one coalesced
+// 256-byte load and store; a[b,t] is the same for the whole wave.
+// ------------------------------------------------------------------------------------------
+constexpr int kBoundaryWaves = 16;
+
+__global__ __launch_bounds__(kBoundaryWaves * 64) void fl_boundary_scan_kernel(
+    const float* __restrict__ a, const float* __restrict__ drive, int T, int R,
+    const float* __restrict__ state_in, float* __restrict__ state_out, float* __restrict__ out) {
+  __shared__ float s_p[kBoundaryWaves][64], s_s[kBoundaryWaves][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int b = blockIdx.x;
+  const int r = blockIdx.y * 64 + lane;
+  const bool ok = r < R;
+  const int span = (T + kBoundaryWaves - 1) / kBoundaryWaves;
+  const int t0 = min(wave * span, T), t1 = min(t0 + span, T);
+  const float* ab = a + (int64_t)b * T;
+  const float* db = drive + (int64_t)b * T * R + r;
+  float* ob = out + (int64_t)b * T * R + r;
+  float p = 1.f, sv = 0.f;
+  for (int t = t0; t < t1; ++t) {
+    const float at = ab[t];
+    const float d = ok ? db[(int64_t)t * R] : 0.f;
+    sv = fmaf(at, sv, d);
+    p *= at;
+  }
+  s_p[wave][lane] = p;
+  s_s[wave][lane] = sv;
+  __syncthreads();
+  float c = (ok && state_in) ? state_in[(int64_t)b * R + r] : 0.f;
+  for (int u = 0; u < wave; ++u) c = fmaf(s_p[u][lane], c, s_s[u][lane]);
+  for (int t = t0; t < t1; ++t) {
+    const float at = ab[t];
+    const float d = ok ? db[(int64_t)t * R] : 0.f;
+    c = fmaf(at, c, d);
+    if (ok) ob[(int64_t)t * R] = c;
+  }
+  if (ok && state_out && wave == kBoundaryWaves - 1) {
+    // the last wave ends at T (or holds the composed carry when its span is empty)
+    state_out[(int64_t)b * R + r] = c;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -1638,6 +1688,21 @@ int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
   FL_DN(float, float)
 #undef FL_DN
 #undef FL_DN1
+}
+
+int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, int64_t R,
+                     const float* state_in, float* state_out, float* out, void* stream) {
+  if (B <= 0 || T <= 0 || R <= 0 || B > kMaxB || R > kMaxC || T > kMaxT)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (T * R >= ((int64_t)1 << 40)) return FL_ERR_INVALID_ARGUMENT;
+  if (!a || !drive || !out) return FL_ERR_INVALID_ARGUMENT;
+  if (!aligned(a, 4) || !aligned(drive, 4) || !aligned(out, 4) ||
+      (state_in && !aligned(state_in, 4)) || (state_out && !aligned(state_out, 4)))
+    return FL_ERR_INVALID_ARGUMENT;
+  const dim3 grid((unsigned)B, (unsigned)cdiv(R, 64));
+  fl_boundary_scan_kernel<<<grid, kBoundaryWaves * 64, 0, static_cast<hipStream_t>(stream)>>>(
+      a, drive, (int)T, (int)R, state_in, state_out, out);
+  return hip_status(hipGetLastError());
 }
 
 }  // extern "C"

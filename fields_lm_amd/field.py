@@ -262,6 +262,39 @@ def field_decode_norm_step(raw_t: torch.Tensor, transition_r: torch.Tensor,
     return out
 
 
+def boundary_scan(a: torch.Tensor, drive: torch.Tensor, state_in: Optional[torch.Tensor] = None,
+                  return_state: bool = False):
+    """Softpatch boundary scan on the HIP path: s[b,t,:] = a[b,t] * s[b,t-1,:] + drive[b,t,:]
+    (``hierarchical_scan(a, drive, 32)`` of v3:458-460 with ``a`` one value per token).
+
+    a [B,T] fp32, drive [B,T,R] fp32, state_in [B,R] or None. Returns s [B,T,R] (and s[:,T-1]).
+    """
+    lib = nat.load()
+    if not (a.is_cuda and drive.is_cuda):
+        raise RuntimeError("the boundary scan requires a ROCm (cuda) device")
+    if drive.ndim != 3 or a.shape != drive.shape[:2]:
+        raise ValueError((tuple(a.shape), tuple(drive.shape)))
+    if a.dtype != torch.float32 or drive.dtype != torch.float32:
+        raise TypeError("a and drive must be float32")
+    a, drive = a.contiguous(), drive.contiguous()
+    batch, length, rank = drive.shape
+    out = torch.empty_like(drive)
+    sout = torch.empty((batch, rank), device=drive.device, dtype=torch.float32) if return_state else None
+    sin = None
+    if state_in is not None:
+        if state_in.shape != (batch, rank):
+            raise ValueError(f"state_in must be [B, R] = {(batch, rank)}")
+        sin = state_in.detach().to(device=drive.device, dtype=torch.float32).contiguous()
+    if batch == 0 or length == 0 or rank == 0:
+        if sout is not None:
+            sout.copy_(sin if sin is not None else torch.zeros_like(sout))
+        return (out, sout) if return_state else out
+    code = lib.fl_boundary_scan(nat.ptr(a), nat.ptr(drive), batch, length, rank, nat.ptr(sin),
+                                nat.ptr(sout), nat.ptr(out), nat.stream_handle(drive.device))
+    nat.check(code, "fl_boundary_scan")
+    return (out, sout) if return_state else out
+
+
 def state_to_complex(state: torch.Tensor) -> torch.Tensor:
     """Planar [B,2C] fp32 state -> complex64 [B,C]."""
     c = state.shape[-1] // 2
@@ -398,16 +431,23 @@ class IndependentVacancyField(nn.Module):
                                      read_dtype=self._read_dtype(raw))
         return self._readout(x, read), new_state
 
+    def decode_params(self) -> Tuple[torch.Tensor, ...]:
+        """(tr, ti, gamma, read_norm weight in fp32): what :meth:`step` reads, cached once per
+        decode loop."""
+        return (*self.transition(), self.read_norm.weight.detach().float().contiguous())
+
     def step(self, x_t: torch.Tensor, state: torch.Tensor,
-             params: Optional[Tuple[torch.Tensor, torch.Tensor, torch.Tensor]] = None) -> torch.Tensor:
+             params: Optional[Tuple[torch.Tensor, ...]] = None) -> torch.Tensor:
         """One decode token: x_t [B,dim] -> [B,dim]; ``state`` [B,2C] fp32 is advanced in place.
 
-        ``params`` = a cached ``self.transition()`` (recomputed when None).
+        ``params`` = a cached ``self.transition()`` or ``self.decode_params()`` (recomputed when
+        None).
         """
-        tr, ti, gamma = params if params is not None else self.transition()
+        params = params if params is not None else self.decode_params()
+        tr, ti, gamma = params[:3]
         raw_t = self._raw(x_t)
         if self._fused():
-            w = self.read_norm.weight.detach().float().contiguous()
+            w = params[3] if len(params) > 3 else self.read_norm.weight.detach().float().contiguous()
             normed = field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
                                             out_dtype=self._read_dtype(raw_t))
             return self._project(x_t, normed)

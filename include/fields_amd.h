@@ -136,6 +136,19 @@ int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
                         const float* gamma, float* state, const float* norm_weight, float eps,
                         void* out_t, int out_dtype, void* stream);
 
+/*
+ * Boundary scan of the softpatch mixer: s[b,t,r] = a[b,t] * s[b,t-1,r] + drive[b,t,r] with
+ * s[b,-1,:] = state_in (or 0), written to out [B, T, R]; state_out [B, R] receives s[b,T-1,:].
+ *
+ * Replaces `hierarchical_scan(a, drive, block=32)` in `BoundaryStateMixer.forward`
+ * (src/fields_official/reference/official_source/field_hybrid_attentionfree_qualification_v3.py:458-460
+ * and field_hybrid_speed_optimization_v6.py:333-335), where a = 1 - boundary is one value per
+ * token broadcast over the rank R. All buffers fp32 and contiguous; state_in / state_out may be
+ * NULL. No workspace.
+ */
+int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, int64_t R,
+                     const float* state_in, float* state_out, float* out, void* stream);
+
 /* Library version string (host function). No counterpart in the reference. */
 const char* fl_version(void);
 

@@ -126,6 +126,16 @@ def test_norm_argument_validation_returns_before_launch(lib):
     assert dn(16, 0, 1, 8, 24, 16, 16, 16, 16, 18, 1e-6, 16, 0, None) == nat.FL_ERR_INVALID_ARGUMENT
 
 
+def test_boundary_scan_validation_returns_before_launch(lib):
+    bs = lib.fl_boundary_scan
+    assert bs(256, 256, 0, 4, 8, None, None, 256, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert bs(256, 256, 1, 0, 8, None, None, 256, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert bs(256, 256, 1, 4, 0, None, None, 256, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert bs(None, 256, 1, 4, 8, None, None, 256, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert bs(256, 256, 1, 4, 8, None, None, None, None) == nat.FL_ERR_INVALID_ARGUMENT
+    assert bs(258, 256, 1, 4, 8, None, None, 256, None) == nat.FL_ERR_INVALID_ARGUMENT  # misaligned
+
+
 def test_error_mapping():
     nat.check(nat.FL_OK, "x")
     with pytest.raises(ValueError):
