@@ -477,9 +477,13 @@ class Mamba2Mixer(nn.Module):
     def forward(self, u: torch.Tensor, return_state: bool = False):
         b, l, _ = u.shape
         z, xbc_raw, dt = self._split(self.in_proj(u))
-        w = self.conv1d.weight.float()
-        xbc = F.conv1d(xbc_raw.float().transpose(1, 2), w, self.conv1d.bias.float(),
-                       padding=self.d_conv - 1, groups=self.conv_dim)[..., :l].transpose(1, 2)
+        # causal depthwise convolution as d_conv shifted multiply-adds in the channel-last
+        # layout: out[t] = bias + sum_k w[k] * in[t - (d_conv-1) + k]
+        w = self.conv1d.weight.float()[:, 0]                                           # [C, K]
+        xp = F.pad(xbc_raw.float(), (0, 0, self.d_conv - 1, 0))
+        xbc = self.conv1d.bias.float() + xp[:, :l] * w[:, 0]
+        for k in range(1, self.d_conv):
+            xbc = torch.addcmul(xbc, xp[:, k:k + l], w[:, k])
         x, bm, cm, dt = self._ssm_in(F.silu(xbc), dt)
         A = -torch.exp(self.A_log.float())
         xh = x.reshape(b, l, self.nheads, self.headdim)

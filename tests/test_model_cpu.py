@@ -177,6 +177,25 @@ def test_mamba2_short_prompt_conv_state():
     torch.testing.assert_close(torch.stack(steps, 1), full[:, 2:], rtol=1e-4, atol=1e-5)
 
 
+def test_mamba2_forward_matches_conv1d_and_recurrence():
+    """The mixer's forward equals torch's causal depthwise conv1d followed by the brute-force
+    SSD recurrence, D skip, gated norm and out_proj."""
+    torch.manual_seed(12)
+    mix = M.Mamba2Mixer(32, d_state=8, d_conv=4, expand=2, headdim=16, chunk_size=8)
+    u = torch.randn(2, 19, 32)
+    with torch.no_grad():
+        z, xbc_raw, dt = mix._split(mix.in_proj(u))
+        xbc = F.conv1d(xbc_raw.transpose(1, 2), mix.conv1d.weight, mix.conv1d.bias, padding=3,
+                       groups=mix.conv_dim)[..., :19].transpose(1, 2)
+        x, bm, cm, dtp = mix._ssm_in(F.silu(xbc), dt)
+        xh = x.reshape(2, 19, mix.nheads, mix.headdim)
+        y, _ = _ssd_naive(xh, dtp, -torch.exp(mix.A_log), bm, cm)
+        y = y.float() + mix.D[:, None] * xh
+        exp = mix.out_proj(mix.norm(y.reshape(2, 19, mix.d_inner), z))
+        got = mix(u)
+    torch.testing.assert_close(got, exp, rtol=1e-4, atol=1e-5)
+
+
 def test_mamba2_init_ranges():
     torch.manual_seed(10)
     mix = M.Mamba2Mixer(1024)
