@@ -17,6 +17,7 @@ read_bf16 (7,168 B/token), norm_bf16 / norm_fp32 (read_norm fused into the epilo
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -265,6 +266,48 @@ def decode_comparison(batch: int = 64, dim: int = 1024, prompt: int = 2048, toke
     }
 
 
+def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
+    """fl_scan_backward on a workload (bf16 raw and bf16 grad_raw, fp32 read / grad_read):
+    algorithmic bytes per token 3C*2 (raw) + 4C*4 (grad_read) + 2C*4 (the read's state planes)
+    + 3C*2 (grad_raw) = 18,432 at C = 512."""
+    import torch
+
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan
+    from fields_lm_amd.workloads import make_scan_workload
+
+    dev = torch.device("cuda:0")
+    wl = make_scan_workload(workload, dev)
+    B, T, C = wl.raw.shape[0], wl.raw.shape[1], wl.channels
+    read = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma)
+    gread = torch.randn(read.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(4))
+    grad_raw = torch.empty(B, T, 3 * C, device=dev, dtype=torch.bfloat16)
+    gp = [torch.empty(C, device=dev) for _ in range(3)]
+    lib = nat.load()
+    n = int(lib.fl_scan_backward_workspace_bytes(B, T, C))
+    ws = torch.zeros(n, device=dev, dtype=torch.uint8)
+    stream = torch.cuda.current_stream(dev)
+    args = (nat.ptr(wl.raw), nat.FL_DTYPE_BF16, B, T, C, wl.raw.stride(0), wl.raw.stride(1), nat.ptr(wl.tr),
+            nat.ptr(wl.ti), nat.ptr(wl.gamma), None, nat.ptr(read), nat.ptr(gread), None, nat.ptr(grad_raw),
+            nat.FL_DTYPE_BF16, *[nat.ptr(x) for x in gp], None, nat.ptr(ws), n,
+            ctypes.c_void_p(stream.cuda_stream))
+
+    class _Plan:
+        device = dev
+
+        def run(self, s=None):
+            nat.check(lib.fl_scan_backward(*args), "fl_scan_backward")
+
+    _, ev = time_plan(_Plan(), steps, warmup)
+    nbytes = (3 * C * 2 + 4 * C * 4 + 2 * C * 4 + 3 * C * 2) * B * T
+    if nat.workspace_error(ws) != 0:
+        raise RuntimeError("backward look-back wait gave up")
+    return {"workload": workload, "us_per_step": ev * 1e3, "tokens_per_s": B * T / (ev * 1e-3),
+            "bytes_per_token": nbytes // (B * T), "gbs": nbytes / (ev * 1e-3) / 1e9,
+            "frac_hbm_peak": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "note": "includes the parameter-gradient reduction launch"}
+
+
 def _promoted_model(dev):
     from fields_lm_amd.model import build_official_fields, cast_for_inference
 
@@ -400,6 +443,33 @@ def model_decode(batch: int = 64, prompt: int = 2048, new_tokens: int = 256):
     }
 
 
+def cpu_backward(workload_name: str, runs: int = 3):
+    """The reference CPU path's backward: torch autograd through the op-for-op restatement of
+    reference_field_read (complex64, block 32) on the host cores, same workload, fp32 raw."""
+    import torch
+
+    import oracle  # noqa: F401  (checker package; timed CPU baseline only)
+    from oracle import reference_path as ref
+    from fields_lm_amd.workloads import make_scan_workload
+
+    wl = make_scan_workload(workload_name, "cuda")
+    raw = wl.raw.float().cpu().requires_grad_()
+    tr, ti, gamma = (t.cpu().requires_grad_() for t in (wl.tr, wl.ti, wl.gamma))
+    gread = torch.randn(raw.shape[0], raw.shape[1], 4 * wl.channels)
+    times = []
+    for i in range(runs + 1):
+        read = ref.field_read(raw, tr, ti, gamma, 32)
+        t0 = time.perf_counter()
+        read.backward(gread)
+        if i:
+            times.append(time.perf_counter() - t0)
+        raw.grad = None
+    med = statistics.median(times)
+    return {"value": wl.tokens / med, "unit": "tokens/s", "s_per_backward": med,
+            "cores": len(os.sched_getaffinity(0)), "kind": "port",
+            "sample": f"{workload_name}: autograd backward of the restated reference CPU path, median of {runs}"}
+
+
 def cpu_decode_reforward(runs: int = 3):
     """Reference CPU path per-token cost of decode: one full-prefix re-forward of the Field block
     (oracle/reference_path.py, the reference's CPU path restated) at B=1, T=2048, fp32."""
@@ -436,6 +506,8 @@ def main() -> int:
     ap.add_argument("--variant", default="read_fp32", choices=list(VARIANTS))
     ap.add_argument("--decode-only", action="store_true",
                     help="only the B=64 decode comparison (kernel and block step in HIP graphs)")
+    ap.add_argument("--backward-only", action="store_true",
+                    help="only the backward scan at config 2 (and config 4)")
     ap.add_argument("--model", choices=["prefill", "decode"],
                     help="only the whole-model run: prefill (config 3) or decode (config 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -464,6 +536,10 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.decode_only:
         print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
+        return 0
+    if args.backward_only:
+        print(json.dumps({"backward": [backward_timing("scan_b8_t2048_d1024"),
+                                       backward_timing("scan_b1_t65536_d1024", steps=20, warmup=3)]}), flush=True)
         return 0
     if args.model:
         fn = model_prefill if args.model == "prefill" else model_decode
@@ -573,6 +649,9 @@ def main() -> int:
                                                "note": "fp32 read, then RMSNorm module, then bf16 cast"}
         del pp, wl, norm
         torch.cuda.empty_cache()
+        extras["backward_b8_t2048"] = backward_timing("scan_b8_t2048_d1024")
+        extras["backward_b1_t65536"] = backward_timing("scan_b1_t65536_d1024", steps=20, warmup=3)
+        torch.cuda.empty_cache()
         extras["decode_b64"] = decode_comparison()
         torch.cuda.empty_cache()
         log("[bench] model prefill (config 3) ...")
@@ -588,6 +667,8 @@ def main() -> int:
         if not args.no_extras:
             log("[bench] cpu decode re-forward ...")
             result["cpu_baseline"]["decode_reforward"] = cpu_decode_reforward()
+            log("[bench] cpu backward ...")
+            result["cpu_baseline"]["backward"] = cpu_backward(args.workload)
 
     print(json.dumps(result), flush=True)
     return 0

@@ -22,6 +22,7 @@ from .field import (  # noqa: F401
     field_decode_norm_step,
     field_decode_step,
     field_scan,
+    field_scan_backward,
     field_scan_norm,
     fused_field_read,
     state_to_complex,

@@ -43,6 +43,9 @@ SIGNATURES = {
     "fl_decode_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _int, _vp]),
     "fl_decode_norm_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                    ctypes.c_float, _vp, _int, _vp]),
+    "fl_scan_backward": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
+                                _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "fl_scan_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "fl_boundary_scan": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),
     "fl_version": (ctypes.c_char_p, []),
 }
@@ -108,10 +111,12 @@ def stream_handle(device: torch.device) -> ctypes.c_void_p:
 _workspaces: dict = {}
 
 
-def scan_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """Zero-filled, 256-byte aligned workspace of at least ``nbytes`` for the current stream."""
+def scan_workspace(device: torch.device, nbytes: int, kind: str = "forward") -> torch.Tensor:
+    """Zero-filled, 256-byte aligned workspace of at least ``nbytes`` for the current stream.
+
+    ``kind`` keeps the forward and backward scans' workspaces apart (their layouts differ)."""
     stream = torch.cuda.current_stream(device)
-    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream)
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
         ws = torch.zeros(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)

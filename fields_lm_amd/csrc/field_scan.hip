@@ -734,6 +734,161 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
   }
 }
 
+// Decoupled look-back of one tile, run by all W waves of the block: composes the published
+// summaries (AGG) of the tile's predecessors ord-1, ord-2, ... in its chain until one with a
+// published inclusive state (INCL) is found. Every predecessor is a full tile, so its map is
+// A = lamT * P. On return wave 0 holds the tile's carry-in in (cr, ci) (unchanged if a wait gave
+// up, with the error bit set). ``ord`` is the tile's position in its chain's processing order.
+template <int K, int W>
+__device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks, const uint32_t* st_chain,
+                                               uint64_t* data, uint32_t tag_agg, uint32_t tag_incl,
+                                               const float* lTr, const float* lTi, bool ok, int lane,
+                                               int wave, LookbackHeader* hdr,
+                                               float (&s_part)[W][4][64 * K],
+                                               float (&s_carry)[2][64 * K], int (&s_meta)[4],
+                                               float* cr, float* ci) {
+  constexpr int CT = 64 * K;
+  constexpr int kMaxRound = W * kLookbackPerWave < 64 ? W * kLookbackPerWave : 64;
+  // acc (wave 0): map from the end of the farthest consumed predecessor to the tile start
+  float aAr[K], aAi[K], aBr[K], aBi[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) { aAr[k] = 1.f; aAi[k] = 0.f; aBr[k] = 0.f; aBi[k] = 0.f; }
+  uint32_t spins = 0;
+  bool failed = false;
+  // Status scan (wave 0): statuses of the 64 predecessors j, j-1, ... in one load; s_meta gets
+  // (j, n, kind): the next round composes the n nearest summaries, then, for kind 2, starts
+  // from the inclusive state of predecessor j-n.
+  auto scan_status = [&](int j) {
+    const int p = j - lane;
+    uint32_t s = 0;
+    if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
+    const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
+    int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
+    int n;
+    if (i0 >= kMaxRound) {
+      n = kMaxRound;
+      kind = 1;
+    } else {
+      n = i0;
+      const uint32_t s_at = __shfl(s, i0);
+      const int p_at = __shfl(p, i0);
+      kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
+    }
+    if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
+  };
+  if (wave == 0) {
+    scan_status(ord - 1);
+    if (lane == 0) s_meta[3] = 0;
+  }
+  // Each round: barrier, every wave composes its share of the n summaries, barrier, wave 0
+  // folds the shares into acc and scans the statuses for the next round.
+  while (true) {
+    __syncthreads();
+    if (s_meta[3]) break;
+    const int jj = s_meta[0], n = s_meta[1], kind = s_meta[2];
+    // this wave composes predecessors jj - i for i in [lo, hi), nearest first
+    const int m = (n + W - 1) / W;
+    const int lo = min(wave * m, n), hi = min(lo + m, n);
+    {
+      float pAr[K], pAi[K], pBr[K], pBi[K];
+#pragma unroll
+      for (int k = 0; k < K; ++k) { pAr[k] = 1.f; pAi[k] = 0.f; pBr[k] = 0.f; pBi[k] = 0.f; }
+      // sub-batches of kLookbackBatch predecessors, nearest first (no barrier in between)
+      for (int q0 = lo; ok && q0 < hi && !failed; q0 += kLookbackBatch) {
+        uint64_t w[kLookbackBatch][3][K];
+#pragma unroll
+        for (int q = 0; q < kLookbackBatch; ++q) {
+          if (q0 + q < hi) {
+            uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              w[q][0][k] = get_word(dp + k);
+              w[q][1][k] = get_word(dp + CT + k);
+              w[q][2][k] = get_word(dp + 2 * CT + k);
+            }
+          }
+        }
+#pragma unroll
+        for (int q = 0; q < kLookbackBatch; ++q) {
+          if (q0 + q < hi && !failed) {
+            uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
+#pragma unroll
+            for (int k = 0; k < K; ++k) {
+              uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
+              if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins)) { failed = true; break; }
+              // partial <- partial o M(pred), with A(pred) = lam^TC * P
+              const float P = word_value(ww[0]);
+              const float ar = P * lTr[k], ai = P * lTi[k];
+              const float qBr = word_value(ww[1]), qBi = word_value(ww[2]);
+              const float nBr = pAr[k] * qBr - pAi[k] * qBi + pBr[k];
+              const float nBi = pAr[k] * qBi + pAi[k] * qBr + pBi[k];
+              const float nAr = pAr[k] * ar - pAi[k] * ai;
+              const float nAi = pAr[k] * ai + pAi[k] * ar;
+              pAr[k] = nAr; pAi[k] = nAi; pBr[k] = nBr; pBi[k] = nBi;
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        s_part[wave][0][lane * K + k] = pAr[k];
+        s_part[wave][1][lane * K + k] = pAi[k];
+        s_part[wave][2][lane * K + k] = pBr[k];
+        s_part[wave][3][lane * K + k] = pBi[k];
+      }
+    }
+    if (kind == 2 && wave == W - 1 && ok) {  // inclusive state of predecessor jj - n
+      uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - n)) * kPlanes * CT + lane * K;
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
+        if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
+        s_carry[0][lane * K + k] = word_value(ww[0]);
+        s_carry[1][lane * K + k] = word_value(ww[1]);
+      }
+    }
+    if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
+    __syncthreads();
+    if (wave == 0) {
+      // acc <- acc o part_0 o part_1 o ...  (part_u covers nearer predecessors than part_u+1)
+      for (int u = 0; u < W; ++u) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int x = lane * K + k;
+          const float qAr = s_part[u][0][x], qAi = s_part[u][1][x];
+          const float qBr = s_part[u][2][x], qBi = s_part[u][3][x];
+          const float nBr = aAr[k] * qBr - aAi[k] * qBi + aBr[k];
+          const float nBi = aAr[k] * qBi + aAi[k] * qBr + aBi[k];
+          const float nAr = aAr[k] * qAr - aAi[k] * qAi;
+          const float nAi = aAr[k] * qAi + aAi[k] * qAr;
+          aAr[k] = nAr; aAi[k] = nAi; aBr[k] = nBr; aBi[k] = nBi;
+        }
+      }
+      int done = 0;
+      if (kind == 2) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int x = lane * K + k;
+          const float sr = s_carry[0][x], si = s_carry[1][x];
+          cr[k] = aAr[k] * sr - aAi[k] * si + aBr[k];
+          ci[k] = aAr[k] * si + aAi[k] * sr + aBi[k];
+        }
+        done = 1;
+      } else if (kind == 0) {
+        if (++spins > kSpinLimit) {
+          failed = true;
+          if (lane == 0) atomicOr(&hdr->error, 1u);
+        }
+        __builtin_amdgcn_s_sleep(2);
+      }
+      if (__ballot(failed) != 0ull) done = 1;  // give up: the carry stays state_in / 0
+      if (!done) scan_status(jj - n);
+      if (lane == 0) s_meta[3] = done;
+    }
+  }
+}
+
 // NORM: out = RMSNorm(read) (canon:300-309 applied to canon:1176-1193's read), norm_w [4C],
 // sib = per-row partials [n_tiles][W*L] words; otherwise out = read and those are unused.
 template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM>
@@ -746,7 +901,6 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
-  constexpr int kMaxRound = W * kLookbackPerWave < 64 ? W * kLookbackPerWave : 64;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
   __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
   __shared__ float s_part[W][4][CT];  // look-back partial maps (Ar, Ai, Br, Bi)
@@ -842,146 +996,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     cr[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
     ci[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
   }
-  if (chunk > 0) {
-    // acc (wave 0): map from the end of the farthest consumed predecessor to the tile start
-    float aAr[K], aAi[K], aBr[K], aBi[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) { aAr[k] = 1.f; aAi[k] = 0.f; aBr[k] = 0.f; aBi[k] = 0.f; }
-    uint32_t spins = 0;
-    bool failed = false;
-    // Status scan (wave 0): statuses of the 64 predecessors j, j-1, ... in one load; s_meta gets
-    // (j, n, kind): the next round composes the n nearest summaries, then, for kind 2, starts
-    // from the inclusive state of predecessor j-n.
-    auto scan_status = [&](int j) {
-      const int p = j - lane;
-      uint32_t s = 0;
-      if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
-      const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
-      int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
-      int n;
-      if (i0 >= kMaxRound) {
-        n = kMaxRound;
-        kind = 1;
-      } else {
-        n = i0;
-        const uint32_t s_at = __shfl(s, i0);
-        const int p_at = __shfl(p, i0);
-        kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
-      }
-      if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
-    };
-    if (wave == 0) {
-      scan_status(chunk - 1);
-      if (lane == 0) s_meta[3] = 0;
-    }
-    // Each round: barrier, every wave composes its share of the n summaries, barrier, wave 0
-    // folds the shares into acc and scans the statuses for the next round.
-    while (true) {
-      __syncthreads();
-      if (s_meta[3]) break;
-      const int jj = s_meta[0], n = s_meta[1], kind = s_meta[2];
-      // this wave composes predecessors jj - i for i in [lo, hi), nearest first
-      const int m = (n + W - 1) / W;
-      const int lo = min(wave * m, n), hi = min(lo + m, n);
-      {
-        float pAr[K], pAi[K], pBr[K], pBi[K];
-#pragma unroll
-        for (int k = 0; k < K; ++k) { pAr[k] = 1.f; pAi[k] = 0.f; pBr[k] = 0.f; pBi[k] = 0.f; }
-        // sub-batches of kLookbackBatch predecessors, nearest first (no barrier in between)
-        for (int q0 = lo; ok && q0 < hi && !failed; q0 += kLookbackBatch) {
-          uint64_t w[kLookbackBatch][3][K];
-#pragma unroll
-          for (int q = 0; q < kLookbackBatch; ++q) {
-            if (q0 + q < hi) {
-              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
-#pragma unroll
-              for (int k = 0; k < K; ++k) {
-                w[q][0][k] = get_word(dp + k);
-                w[q][1][k] = get_word(dp + CT + k);
-                w[q][2][k] = get_word(dp + 2 * CT + k);
-              }
-            }
-          }
-#pragma unroll
-          for (int q = 0; q < kLookbackBatch; ++q) {
-            if (q0 + q < hi && !failed) {
-              uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
-#pragma unroll
-              for (int k = 0; k < K; ++k) {
-                uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
-                if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins)) { failed = true; break; }
-                // partial <- partial o M(pred), with A(pred) = lam^TC * P
-                const float P = word_value(ww[0]);
-                const float ar = P * lTr[k], ai = P * lTi[k];
-                const float qBr = word_value(ww[1]), qBi = word_value(ww[2]);
-                const float nBr = pAr[k] * qBr - pAi[k] * qBi + pBr[k];
-                const float nBi = pAr[k] * qBi + pAi[k] * qBr + pBi[k];
-                const float nAr = pAr[k] * ar - pAi[k] * ai;
-                const float nAi = pAr[k] * ai + pAi[k] * ar;
-                pAr[k] = nAr; pAi[k] = nAi; pBr[k] = nBr; pBi[k] = nBi;
-              }
-            }
-          }
-        }
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          s_part[wave][0][lane * K + k] = pAr[k];
-          s_part[wave][1][lane * K + k] = pAi[k];
-          s_part[wave][2][lane * K + k] = pBr[k];
-          s_part[wave][3][lane * K + k] = pBi[k];
-        }
-      }
-      if (kind == 2 && wave == W - 1 && ok) {  // inclusive state of predecessor jj - n
-        uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - n)) * kPlanes * CT + lane * K;
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
-          if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
-          s_carry[0][lane * K + k] = word_value(ww[0]);
-          s_carry[1][lane * K + k] = word_value(ww[1]);
-        }
-      }
-      if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
-      __syncthreads();
-      if (wave == 0) {
-        // acc <- acc o part_0 o part_1 o ...  (part_u covers nearer predecessors than part_u+1)
-        for (int u = 0; u < W; ++u) {
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const int x = lane * K + k;
-            const float qAr = s_part[u][0][x], qAi = s_part[u][1][x];
-            const float qBr = s_part[u][2][x], qBi = s_part[u][3][x];
-            const float nBr = aAr[k] * qBr - aAi[k] * qBi + aBr[k];
-            const float nBi = aAr[k] * qBi + aAi[k] * qBr + aBi[k];
-            const float nAr = aAr[k] * qAr - aAi[k] * qAi;
-            const float nAi = aAr[k] * qAi + aAi[k] * qAr;
-            aAr[k] = nAr; aAi[k] = nAi; aBr[k] = nBr; aBi[k] = nBi;
-          }
-        }
-        int done = 0;
-        if (kind == 2) {
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const int x = lane * K + k;
-            const float sr = s_carry[0][x], si = s_carry[1][x];
-            cr[k] = aAr[k] * sr - aAi[k] * si + aBr[k];
-            ci[k] = aAr[k] * si + aAi[k] * sr + aBi[k];
-          }
-          done = 1;
-        } else if (kind == 0) {
-          if (++spins > kSpinLimit) {
-            failed = true;
-            if (lane == 0) atomicOr(&hdr->error, 1u);
-          }
-          __builtin_amdgcn_s_sleep(2);
-        }
-        if (__ballot(failed) != 0ull) done = 1;  // give up: the carry stays state_in / 0
-        if (!done) scan_status(jj - n);
-        if (lane == 0) s_meta[3] = done;
-      }
-    }
-  }
+  if (chunk > 0)
+    lookback_carry<K, W>(chunk, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi, ok, lane,
+                         wave, hdr, s_part, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1077,6 +1094,343 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward scan (fl_scan_backward): the adjoint of the forward recurrence (canon:625-910,
+// 1020-1105), one launch, tiles taken in reverse time order.
+//
+// With U_t = dL/ds_t and D_t = dL/d disp_t (grad_read), the gradient reaching s_t from later
+// steps, c_t, obeys (a_t = (1 - v_t) lam, conj = complex conjugate)
+//   G_t = U_t + c_t,    c_{t-1} = conj(a_t) G_t + conj(v_t lam) D_t
+//                              = conj(lam) [(1 - v_t)(c_t + U_t) + v_t D_t],    c_{T-1} = grad_state_out,
+// a diagonal affine recurrence like the forward one: n steps map c to conj(lam)^n prod(1-v) c + Q.
+// Tiles summarise, publish and look back as in the forward pass, with processing position
+// ord = n_chunks - 1 - chunk; the only partial tile (the end of the sequence) is ord 0, which
+// never publishes a summary. Per step, with p = s_{t-1} (the forward read, state_in at t = 0):
+//   dzr = gamma v Re(G) (1 - tanh^2 zr),  dzi = gamma v Im(G) (1 - tanh^2 zi),
+//   dv  = Re(conj(D) lam p) - Re(conj(G) lam p) + gamma Re(conj(G) inj),  dzv = dv v (1 - v/0.9),
+//   dlam += (1 - v) G conj(p) + v D conj(p),   dgamma += v Re(conj(G) inj),
+// and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
+// then the waves in order) into per-tile partials that fl_param_grad_reduce_kernel adds up over
+// the tiles of each channel in a fixed order (deterministic).
+// ------------------------------------------------------------------------------------------
+template <typename RawT, typename GradT, int K, int L, int W, int OCC>
+__global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
+    const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
+    int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
+    const float* __restrict__ gamma, const float* __restrict__ state_in,
+    const float* __restrict__ read, const float* __restrict__ grad_read,
+    const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
+    float* __restrict__ grad_state_in, float* __restrict__ pgrad, LookbackHeader* hdr,
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
+  constexpr int CT = 64 * K;
+  constexpr int TC = W * L;
+  static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
+  __shared__ float s_sum[W][3][CT];   // wave maps (P, Qr, Qi)
+  __shared__ float s_part[W][4][CT];  // look-back partial maps; then parameter-gradient partials
+  __shared__ float s_carry[2][CT];
+  __shared__ int s_meta[4];
+  __shared__ uint32_t s_tk[2];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  if (threadIdx.x == 0) {
+    const uint32_t x = blockIdx.x % n_split;
+    const unsigned long long tk = atomicAdd(&hdr->ticket[x][0], 1ull);
+    s_tk[0] = (uint32_t)tk * n_split + x;
+    s_tk[1] = (uint32_t)(tk >> 32);
+  }
+  __syncthreads();
+  const uint32_t ticket = s_tk[0];
+  const uint32_t epoch = s_tk[1];
+  if (ticket >= n_tiles) {
+    if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
+    return;
+  }
+  const uint32_t n_chains = n_tiles / (uint32_t)n_chunks;
+  const int ord = (int)(ticket / n_chains);
+  const int chain = (int)(ticket - (uint32_t)ord * n_chains);
+  const int chunk = n_chunks - 1 - ord;
+  const int b = chain / n_ctiles;
+  const int ctile = chain - b * n_ctiles;
+  const int c0 = ctile * CT + lane * K;
+  const bool ok = c0 < C;
+  const uint32_t tag_agg = ((epoch & 0x3fffffffu) << 2) | kTagAgg;
+  const uint32_t tag_incl = ((epoch & 0x3fffffffu) << 2) | kTagIncl;
+  const int t_begin = chunk * TC;
+  const bool last_ord = ord == n_chunks - 1;
+
+  float lr[K], li[K], gm[K], clr[K], cli[K];
+  load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
+#pragma unroll
+  for (int k = 0; k < K; ++k) { clr[k] = lr[k]; cli[k] = -li[k]; }
+  const int w0 = t_begin + wave * L;
+  const int n_valid = min(max(T - w0, 0), L);
+
+  // buffers from row t_begin of batch row b: raw (rows of st elements), grad_read (rows of 4C)
+  const int rows = T - t_begin;
+  const rsrc_t r_raw = make_rsrc(raw + (int64_t)b * sb + (int64_t)t_begin * st,
+                                 (uint32_t)(((int64_t)(rows - 1) * st + 3 * (int64_t)C) * sizeof(RawT)));
+  const rsrc_t r_grd = make_rsrc(grad_read + ((int64_t)b * T + t_begin) * 4 * C,
+                                 (uint32_t)((int64_t)rows * 4 * C * 4));
+  const rsrc_t r_out = make_rsrc(grad_raw + ((int64_t)b * T + t_begin) * 3 * C,
+                                 (uint32_t)((int64_t)rows * 3 * C * sizeof(GradT)));
+  const int vo_raw = c0 * (int)sizeof(RawT), vo_f = c0 * 4, vo_out = c0 * (int)sizeof(GradT);
+  const int raw_row = (int)(st * (int64_t)sizeof(RawT)), raw_plane = C * (int)sizeof(RawT);
+  const int grd_row = 4 * C * 4, f_plane = C * 4;
+  const int out_row = 3 * C * (int)sizeof(GradT), out_plane = C * (int)sizeof(GradT);
+
+  // this wave's rows: U, D (grad_read) and v (from z_v), kept for both passes
+  float uR[L][K], uI[L][K], dR[L][K], dI[L][K], gv[L][K];
+#pragma unroll
+  for (int j = 0; j < L; ++j) {
+    const int so = (wave * L + j) * grd_row;
+    RawLoad<float, K>::run(r_grd, vo_f, so, uR[j]);
+    RawLoad<float, K>::run(r_grd, vo_f, so + f_plane, uI[j]);
+    RawLoad<float, K>::run(r_grd, vo_f, so + 2 * f_plane, dR[j]);
+    RawLoad<float, K>::run(r_grd, vo_f, so + 3 * f_plane, dI[j]);
+    float zv[K];
+    RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + 2 * raw_plane, zv);
+#pragma unroll
+    for (int k = 0; k < K; ++k)
+      gv[j][k] = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv[k] * -kLog2e));
+  }
+  {
+    // wave map from its right edge to its left edge over its valid rows (reverse order)
+    float P[K], Qr[K], Qi[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) { P[k] = 1.f; Qr[k] = 0.f; Qi[k] = 0.f; }
+#pragma unroll
+    for (int j = L - 1; j >= 0; --j) {
+      if (j < n_valid) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const float keep = 1.f - gv[j][k];
+          const float xr = fmaf(keep, Qr[k] + uR[j][k], gv[j][k] * dR[j][k]);
+          const float xi = fmaf(keep, Qi[k] + uI[j][k], gv[j][k] * dI[j][k]);
+          Qr[k] = clr[k] * xr - cli[k] * xi;
+          Qi[k] = clr[k] * xi + cli[k] * xr;
+          P[k] *= keep;
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      s_sum[wave][0][lane * K + k] = P[k];
+      s_sum[wave][1][lane * K + k] = Qr[k];
+      s_sum[wave][2][lane * K + k] = Qi[k];
+    }
+  }
+  float cLr[K], cLi[K], cTr[K], cTi[K];  // conj(lam)^L, conj(lam)^TC
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    cpow(clr[k], cli[k], L, cLr[k], cLi[k]);
+    cpow(cLr[k], cLi[k], W, cTr[k], cTi[k]);
+  }
+  // conj(lam)^(valid rows of wave u): L except in the (partial) last tile of the sequence
+  auto wave_pow = [&](int u, int k, float& pr, float& pi) {
+    const int nu = min(max(T - (t_begin + u * L), 0), L);
+    if (nu == L) { pr = cLr[k]; pi = cLi[k]; } else { cpow(clr[k], cli[k], nu, pr, pi); }
+  };
+  __syncthreads();
+
+  const uint32_t tile_id = (uint32_t)chain * (uint32_t)n_chunks + (uint32_t)ord;
+  uint32_t* st_chain = status + (size_t)chain * n_chunks;
+  uint64_t* dt = data + (size_t)tile_id * kPlanes * CT + lane * K;
+  if (wave == 0 && ord > 0 && !last_ord) {  // full tile with a successor: publish its map
+    float TP[K], TBr[K], TBi[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) { TP[k] = 1.f; TBr[k] = 0.f; TBi[k] = 0.f; }
+    for (int u = W - 1; u >= 0; --u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int x = lane * K + k;
+        apply_map(cLr[k], cLi[k], s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], TBr[k], TBi[k]);
+        TP[k] *= s_sum[u][0][x];
+      }
+    }
+    if (ok) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        put_word(dt + 0 * CT + k, TP[k], tag_agg);
+        put_word(dt + 1 * CT + k, TBr[k], tag_agg);
+        put_word(dt + 2 * CT + k, TBi[k], tag_agg);
+      }
+    }
+    if (lane == 0)
+      __hip_atomic_store(st_chain + ord, tag_agg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+
+  float cr[K], ci[K];  // carry entering the tile's last row
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    cr[k] = (ok && grad_state_out) ? grad_state_out[(int64_t)b * 2 * C + c0 + k] : 0.f;
+    ci[k] = (ok && grad_state_out) ? grad_state_out[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
+  }
+  if (ord > 0)
+    lookback_carry<K, W>(ord, chain, n_chunks, st_chain, data, tag_agg, tag_incl, cTr, cTi, ok, lane,
+                         wave, hdr, s_part, s_carry, s_meta, cr, ci);
+  if (wave == 0) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      s_carry[0][lane * K + k] = cr[k];
+      s_carry[1][lane * K + k] = ci[k];
+    }
+    if (!last_ord) {  // the carry leaving the tile's first row, for the tile before it in time
+      if (ok) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          float sr = cr[k], si = ci[k];
+          for (int u = W - 1; u >= 0; --u) {
+            const int x = lane * K + k;
+            float pr, pi;
+            wave_pow(u, k, pr, pi);
+            apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr, si);
+          }
+          put_word(dt + 3 * CT + k, sr, tag_incl);
+          put_word(dt + 4 * CT + k, si, tag_incl);
+        }
+      }
+      if (lane == 0)
+        __hip_atomic_store(st_chain + ord, tag_incl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+
+  float gtr[K], gti[K], ggm[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) { gtr[k] = 0.f; gti[k] = 0.f; ggm[k] = 0.f; }
+  if (n_valid > 0) {
+    float car[K], cai[K];  // carry entering this wave's last valid row
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      car[k] = s_carry[0][lane * K + k];
+      cai[k] = s_carry[1][lane * K + k];
+    }
+    for (int u = W - 1; u > wave; --u) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int x = lane * K + k;
+        float pr, pi;
+        wave_pow(u, k, pr, pi);
+        apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], car[k], cai[k]);
+      }
+    }
+#pragma unroll
+    for (int j = L - 1; j >= 0; --j) {
+      if (j < n_valid) {
+        const int t = w0 + j;
+        float zr[K], zi[K], pr[K], pi[K];
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr);
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi);
+        if (t > 0) {
+          const float* prow = read + ((int64_t)b * T + t - 1) * 4 * C + c0;
+#pragma unroll
+          for (int k = 0; k < K; ++k) { pr[k] = ok ? prow[k] : 0.f; pi[k] = ok ? prow[C + k] : 0.f; }
+        } else {
+#pragma unroll
+          for (int k = 0; k < K; ++k) {
+            pr[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
+            pi[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
+          }
+        }
+        float ozr[K], ozi[K], ozv[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const float v = gv[j][k], keep = 1.f - v;
+          const float ur = __builtin_amdgcn_exp2f(fabsf(zr[k]) * (-2.0f * kLog2e));
+          const float ui = __builtin_amdgcn_exp2f(fabsf(zi[k]) * (-2.0f * kLog2e));
+          const float er = 1.0f + ur, ei = 1.0f + ui;
+          const float rdi = __builtin_amdgcn_rcpf(er * ei);
+          const float injr = copysignf((1.0f - ur) * (ei * rdi), zr[k]);
+          const float inji = copysignf((1.0f - ui) * (er * rdi), zi[k]);
+          const float Gr = uR[j][k] + car[k], Gi = uI[j][k] + cai[k];
+          const float mr = lr[k] * pr[k] - li[k] * pi[k];     // lam p
+          const float mi = lr[k] * pi[k] + li[k] * pr[k];
+          const float cb = injr * Gr + inji * Gi;             // Re(conj(G) inj)
+          const float dv = (dR[j][k] * mr + dI[j][k] * mi) - (Gr * mr + Gi * mi) + gm[k] * cb;
+          gtr[k] += keep * (Gr * pr[k] + Gi * pi[k]) + v * (dR[j][k] * pr[k] + dI[j][k] * pi[k]);
+          gti[k] += keep * (Gi * pr[k] - Gr * pi[k]) + v * (dI[j][k] * pr[k] - dR[j][k] * pi[k]);
+          ggm[k] += v * cb;
+          const float gvv = gm[k] * v;
+          ozr[k] = gvv * Gr * (1.0f - injr * injr);
+          ozi[k] = gvv * Gi * (1.0f - inji * inji);
+          ozv[k] = dv * v * (1.0f - v * (1.0f / kVacancyMax));
+          const float xr = fmaf(keep, Gr, v * dR[j][k]);
+          const float xi = fmaf(keep, Gi, v * dI[j][k]);
+          car[k] = clr[k] * xr - cli[k] * xi;
+          cai[k] = clr[k] * xi + cli[k] * xr;
+        }
+        if (ok) {  // lanes past C would land in the next plane of the row
+          const int so = (wave * L + j) * out_row;
+          ReadStore<GradT, K>::run(r_out, vo_out, so, ozr);
+          ReadStore<GradT, K>::run(r_out, vo_out, so + out_plane, ozi);
+          ReadStore<GradT, K>::run(r_out, vo_out, so + 2 * out_plane, ozv);
+        }
+      }
+    }
+    if (w0 == 0 && grad_state_in != nullptr && ok) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        grad_state_in[(int64_t)b * 2 * C + c0 + k] = car[k];
+        grad_state_in[(int64_t)b * 2 * C + C + c0 + k] = cai[k];
+      }
+    }
+  }
+  // parameter-gradient partials of the tile: waves summed in order
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    s_part[wave][0][lane * K + k] = gtr[k];
+    s_part[wave][1][lane * K + k] = gti[k];
+    s_part[wave][2][lane * K + k] = ggm[k];
+  }
+  __syncthreads();
+  if (wave == 0 && ok) {
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      const int x = lane * K + k;
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+      for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
+      float* pg = pgrad + ((size_t)chain * n_chunks + chunk) * 3 * CT + x;
+      pg[0] = a0;
+      pg[CT] = a1;
+      pg[2 * CT] = a2;
+    }
+  }
+
+  // the last block of the launch re-arms the counters for the next launch (next epoch)
+  if (threadIdx.x == 0) {
+    const unsigned int d = atomicAdd(&hdr->done, 1u);
+    if (d == n_tiles - 1) {
+      const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
+      for (int x = 0; x < kTicketCounters; ++x)
+        __hip_atomic_store(&hdr->ticket[x][0], armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+// Sum of the per-tile parameter-gradient partials over the batch rows and chunks of each
+// channel, in a fixed order: grad_tr/ti/gamma[c] (overwritten).
+__global__ __launch_bounds__(256) void fl_param_grad_reduce_kernel(
+    const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT,
+    float* __restrict__ grad_tr, float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  const int ctile = c / CT, x = c - ctile * CT;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+  for (int b = 0; b < B; ++b) {
+    const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks) * 3 * CT + x;
+    for (int k = 0; k < n_chunks; ++k) {
+      a0 += row[(size_t)k * 3 * CT];
+      a1 += row[(size_t)k * 3 * CT + CT];
+      a2 += row[(size_t)k * 3 * CT + 2 * CT];
+    }
+  }
+  grad_tr[c] = a0;
+  grad_ti[c] = a1;
+  grad_gamma[c] = a2;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1515,6 +1869,53 @@ size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
   return workspace_layout(B, T, C).bytes;
 }
 
+// Backward tiling (K channels per lane, L steps per wave, W waves, OCC waves per SIMD) and its
+// workspace: [header 2 KiB][status: tiles x u32][data: tiles x 5 x CT x u64][partials: tiles x 3 x CT x f32]
+constexpr LookbackTiling kBwdTiling = {1, 8, 8, 4};
+
+struct BwdLayout {
+  LookbackGeom g;
+  size_t status_off, data_off, pgrad_off, bytes;
+};
+
+BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
+  BwdLayout w;
+  const int CT = 64 * kBwdTiling.k;
+  w.g = lookback_geom(B, T, C, CT, kBwdTiling.l * kBwdTiling.w);
+  w.status_off = kHeaderBytes;
+  w.data_off = w.status_off + (size_t)cdiv((int64_t)w.g.n_tiles * 4, 256) * 256;
+  w.pgrad_off = w.data_off + (size_t)cdiv((int64_t)w.g.n_tiles * kPlanes * CT * 8, 256) * 256;
+  w.bytes = w.pgrad_off + (size_t)w.g.n_tiles * 3 * CT * sizeof(float);
+  return w;
+}
+
+template <typename RawT, typename GradT>
+int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
+                    const float* tr, const float* ti, const float* gamma, const float* state_in,
+                    const float* read, const float* grad_read, const float* grad_state_out,
+                    void* grad_raw, float* grad_tr, float* grad_ti, float* grad_gamma,
+                    float* grad_state_in, void* workspace, hipStream_t stream) {
+  constexpr LookbackTiling tl = kBwdTiling;
+  constexpr int CT = 64 * tl.k;
+  const BwdLayout lay = bwd_layout(B, T, C);
+  const LookbackGeom& g = lay.g;
+  char* ws = static_cast<char*>(workspace);
+  const int64_t n_chains = B * (int64_t)g.n_ctiles;
+  uint32_t n_split = g.n_chunks <= 64 ? kTicketCounters : 1;
+  while (n_chains % n_split) n_split /= 2;
+  float* pgrad = reinterpret_cast<float*>(ws + lay.pgrad_off);
+  fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ><<<g.n_tiles, tl.w * 64, 0, stream>>>(
+      static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma,
+      state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad,
+      reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
+      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_status(e);
+  fl_param_grad_reduce_kernel<<<(unsigned)cdiv(C, 256), 256, 0, stream>>>(
+      pgrad, (int)B, (int)C, g.n_chunks, g.n_ctiles, CT, grad_tr, grad_ti, grad_gamma);
+  return hip_status(hipGetLastError());
+}
+
 }  // namespace
 
 extern "C" {
@@ -1688,6 +2089,51 @@ int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
   FL_DN(float, float)
 #undef FL_DN
 #undef FL_DN1
+}
+
+size_t fl_scan_backward_workspace_bytes(int64_t B, int64_t T, int64_t C) {
+  if (B <= 0 || T <= 0 || C <= 0) return 0;
+  return bwd_layout(B, T, C).bytes;
+}
+
+int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
+                     const float* gamma, const float* state_in, const float* read,
+                     const float* grad_read, const float* grad_state_out, void* grad_raw,
+                     int grad_raw_dtype, float* grad_tr, float* grad_ti, float* grad_gamma,
+                     float* grad_state_in, void* workspace, size_t workspace_bytes_given,
+                     void* stream) {
+  if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
+  if (grad_raw_dtype != FL_DTYPE_F32 && grad_raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
+  if (B <= 0 || T <= 0 || C <= 0 || B > kMaxB || C > kMaxC || T > kMaxT)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (raw_stride_t < 3 * C || raw_stride_b < 0) return FL_ERR_INVALID_ARGUMENT;
+  if (B > 1 && raw_stride_b < (T - 1) * raw_stride_t + 3 * C) return FL_ERR_INVALID_ARGUMENT;
+  const int64_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  const int64_t gsz = grad_raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * 4 > kMaxBufferBytes)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (raw_stride_t * esz > kMaxRowBytes || 4 * C * 4 > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
+  if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
+  if (!raw || !tr || !ti || !gamma || !read || !grad_read || !grad_raw || !grad_tr || !grad_ti ||
+      !grad_gamma)
+    return FL_ERR_INVALID_ARGUMENT;
+  if (!workspace || workspace_bytes_given < bwd_layout(B, T, C).bytes) return FL_ERR_WORKSPACE;
+  if (!aligned(raw, esz) || !aligned(grad_raw, gsz) || !aligned(workspace, 256) ||
+      !aligned(read, 4) || !aligned(grad_read, 4) || (state_in && !aligned(state_in, 4)) ||
+      (grad_state_out && !aligned(grad_state_out, 4)) || (grad_state_in && !aligned(grad_state_in, 4)))
+    return FL_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+#define FL_BW(R, G)                                                                              \
+  return launch_backward<R, G>(raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, \
+                               read, grad_read, grad_state_out, grad_raw, grad_tr, grad_ti,       \
+                               grad_gamma, grad_state_in, workspace, s);
+  const bool raw16 = raw_dtype == FL_DTYPE_BF16, g16 = grad_raw_dtype == FL_DTYPE_BF16;
+  if (raw16 && g16) { FL_BW(bf16_bits, bf16_bits) }
+  if (raw16) { FL_BW(bf16_bits, float) }
+  if (g16) { FL_BW(float, bf16_bits) }
+  FL_BW(float, float)
+#undef FL_BW
 }
 
 int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, int64_t R,

@@ -150,22 +150,77 @@ def field_scan_norm(raw: torch.Tensor, transition_r: torch.Tensor, transition_i:
                       launch)
 
 
+def field_scan_backward(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
+                        gamma: torch.Tensor, read: torch.Tensor, grad_read: torch.Tensor,
+                        state_in: Optional[torch.Tensor] = None,
+                        grad_state_out: Optional[torch.Tensor] = None,
+                        return_state_grad: bool = False):
+    """Gradients of :func:`field_scan` (``fl_scan_backward``; canon:1020-1105): given the forward's
+    fp32 ``read`` and dL/dread (and dL/dstate_out), returns (grad_raw in raw's dtype, grad_tr,
+    grad_ti, grad_gamma [C] fp32[, grad_state_in [B,2C]])."""
+    lib = nat.load()
+    batch, length, channels = _check_scan_inputs(raw, transition_r)
+    if raw.stride(2) != 1:
+        raw = raw.contiguous()
+    dev = raw.device
+    if read.shape != (batch, length, 4 * channels) or read.dtype != torch.float32:
+        raise ValueError("read must be the forward's fp32 [B, T, 4C] output")
+    if grad_read.shape != read.shape:
+        raise ValueError("grad_read must match read")
+    tr, ti, gm = (t.detach().to(device=dev, dtype=torch.float32).contiguous()
+                  for t in (transition_r, transition_i, gamma))
+    read = read.detach().contiguous()
+    grad_read = grad_read.detach().to(dtype=torch.float32).contiguous()
+    sin = None if state_in is None else state_in.detach().to(device=dev, dtype=torch.float32).contiguous()
+    gso = None if grad_state_out is None else grad_state_out.detach().to(device=dev, dtype=torch.float32).contiguous()
+    for name, t in (("state_in", sin), ("grad_state_out", gso)):
+        if t is not None and t.shape != (batch, 2 * channels):
+            raise ValueError(f"{name} must be [B, 2C]")
+    grad_raw = torch.empty((batch, length, 3 * channels), device=dev, dtype=raw.dtype)
+    g_tr, g_ti, g_gm = (torch.zeros(channels, device=dev, dtype=torch.float32) for _ in range(3))
+    g_sin = torch.zeros((batch, 2 * channels), device=dev, dtype=torch.float32) if return_state_grad else None
+    if batch and length and channels:
+        ws_bytes = int(lib.fl_scan_backward_workspace_bytes(batch, length, channels))
+        ws = nat.scan_workspace(dev, ws_bytes, "backward")
+        code = lib.fl_scan_backward(
+            nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
+            raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin), nat.ptr(read),
+            nat.ptr(grad_read), nat.ptr(gso), nat.ptr(grad_raw), nat.dtype_code(grad_raw.dtype),
+            nat.ptr(g_tr), nat.ptr(g_ti), nat.ptr(g_gm), nat.ptr(g_sin), nat.ptr(ws), ws.numel(),
+            nat.stream_handle(dev))
+        nat.check(code, "fl_scan_backward")
+    elif g_sin is not None and gso is not None:
+        g_sin.copy_(gso)
+    out = (grad_raw, g_tr, g_ti, g_gm)
+    return (*out, g_sin) if return_state_grad else out
+
+
 class _FieldReadFunction(torch.autograd.Function):
-    """Forward of canon:912-1018 on the HIP path. The backward kernels are not built yet."""
+    """canon:912-1105 on the HIP path: forward ``fl_scan_forward``, backward ``fl_scan_backward``.
+
+    When a gradient is needed the fp32 ``read`` is what gets saved (the backward reads the states
+    in fp32); a bf16 ``read_dtype`` then returns its rounded copy."""
 
     @staticmethod
     def forward(ctx, raw, transition_r, transition_i, gamma, block_c, chunk_t,
                 read_dtype=torch.float32):
-        return field_scan(raw, transition_r, transition_i, gamma, read_dtype=read_dtype)
+        if not any(ctx.needs_input_grad[:4]):
+            return field_scan(raw, transition_r, transition_i, gamma, read_dtype=read_dtype)
+        read = field_scan(raw, transition_r, transition_i, gamma)
+        ctx.save_for_backward(raw, transition_r, transition_i, gamma, read)
+        return read if read_dtype == torch.float32 else read.to(read_dtype)
 
     @staticmethod
-    def backward(ctx, *grad_outputs):
-        raise NotImplementedError(
-            "the HIP Field scan is forward-only: its backward (canon:1020-1105) is not implemented")
+    def backward(ctx, grad_read):
+        raw, tr, ti, gamma, read = ctx.saved_tensors
+        grad_raw, g_tr, g_ti, g_gm = field_scan_backward(raw, tr, ti, gamma, read, grad_read)
+        return grad_raw, g_tr.to(tr.dtype), g_ti.to(ti.dtype), g_gm.to(gamma.dtype), None, None, None
 
 
 class _FieldNormReadFunction(torch.autograd.Function):
-    """Forward of read_norm(fused_field_read(...)) on the HIP path; no backward yet."""
+    """Forward of read_norm(fused_field_read(...)) on the HIP path, for inference: the fused
+    epilogue never writes ``read``, so there is nothing to differentiate through (the modules
+    take the unfused path whenever a gradient is needed)."""
 
     @staticmethod
     def forward(ctx, raw, transition_r, transition_i, gamma, weight, eps, out_dtype):
@@ -395,8 +450,15 @@ class IndependentVacancyField(nn.Module):
         gate = torch.sigmoid(self.gate_proj(x))
         return x + (out * gate).to(x.dtype)
 
-    def _fused(self) -> bool:
-        return self.fuse_read_norm and type(self.read_norm) is RMSNorm and self.channels <= 4096
+    def _fused(self, x: Optional[torch.Tensor] = None) -> bool:
+        """read_norm inside the scan kernel: inference only (no gradient needed), the reference's
+        RMSNorm module, C <= 4096."""
+        if not (self.fuse_read_norm and type(self.read_norm) is RMSNorm and self.channels <= 4096):
+            return False
+        if torch.is_grad_enabled() and ((x is not None and x.requires_grad)
+                                        or any(p.requires_grad for p in self.parameters())):
+            return False
+        return True
 
     def _read_dtype(self, raw: torch.Tensor) -> torch.dtype:
         if self.read_dtype == "auto":
@@ -406,7 +468,7 @@ class IndependentVacancyField(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         tr, ti, gamma = self.transition()
         raw = self._raw(x)
-        if self._fused():
+        if self._fused(x):
             normed = _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
                                                   self.read_norm.eps, self._read_dtype(raw))
             return self._project(x, normed)
@@ -422,7 +484,7 @@ class IndependentVacancyField(nn.Module):
         """
         tr, ti, gamma = self.transition()
         raw = self._raw(x)
-        if self._fused():
+        if self._fused(x):
             normed, new_state = field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight,
                                                 self.read_norm.eps, state_in=state,
                                                 return_state=True, out_dtype=self._read_dtype(raw))
@@ -446,7 +508,7 @@ class IndependentVacancyField(nn.Module):
         params = params if params is not None else self.decode_params()
         tr, ti, gamma = params[:3]
         raw_t = self._raw(x_t)
-        if self._fused():
+        if self._fused(x_t):
             w = params[3] if len(params) > 3 else self.read_norm.weight.detach().float().contiguous()
             normed = field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
                                             out_dtype=self._read_dtype(raw_t))

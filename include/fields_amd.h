@@ -103,6 +103,36 @@ int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, i
                          int out_dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Backward of fl_scan_forward: the gradients of a loss L given dL/dread (and dL/dstate_out).
+ *
+ * Replaces `_ChunkedFieldReadFunction.backward`
+ * (field_only_v4_chunked_triton_wiki100.py:1020-1105; Triton kernels 625-910: chunk summary,
+ * chunk carry, chunk materialise, then a torch sum of the parameter partials). One launch for the
+ * reverse scan (decoupled look-back over chunks taken in reverse time order) plus one for the
+ * deterministic reduction of the parameter gradients.
+ *
+ *   raw, strides, tr, ti, gamma, state_in   as given to the forward call
+ *   read            [B, T, 4C] fp32, the forward output (its state planes are read)
+ *   grad_read       [B, T, 4C] fp32 contiguous
+ *   grad_state_out  [B, 2C] fp32 planar, or NULL (state_out unused)
+ *   grad_raw        [B, T, 3C] contiguous, grad_raw_dtype F32 or BF16 (overwritten)
+ *   grad_tr, grad_ti, grad_gamma  [C] fp32 (overwritten)
+ *   grad_state_in   [B, 2C] fp32 planar, or NULL
+ *   workspace       >= fl_scan_backward_workspace_bytes(B, T, C), 256-byte aligned, zero-filled
+ *                   before first use, then reused (one per stream), as for fl_scan_forward
+ */
+int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
+                     const float* gamma, const float* state_in, const float* read,
+                     const float* grad_read, const float* grad_state_out, void* grad_raw,
+                     int grad_raw_dtype, float* grad_tr, float* grad_ti, float* grad_gamma,
+                     float* grad_state_in, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace size in bytes for fl_scan_backward (host function, no device call). Replaces the
+ * ten [B, n_chunks, C] torch.empty buffers of field_only_v4_chunked_triton_wiki100.py:1027-1037. */
+size_t fl_scan_backward_workspace_bytes(int64_t B, int64_t T, int64_t C);
+
+/*
  * Workspace size in bytes for fl_scan_forward at this shape (host function, no device call).
  * Replaces the six [B, n_chunks, C] fp32 torch.empty buffers of
  * field_only_v4_chunked_triton_wiki100.py:941-952.

@@ -11,6 +11,9 @@ Contents
   (src/fields_official/reference/field_only_v4_chunked_triton_wiki100.py:392-416).
 * :func:`rms_norm_f64` — float64 ``RMSNorm`` (same file, 300-309), the mixer's ``read_norm``
   applied to ``read`` (1193): the checker of the fused scan epilogue.
+* :func:`scan_f64_autograd` — the same recurrence as differentiable float64 torch ops
+  (complex128 doubling scan), whose autograd gradients are the checker of the backward scan
+  (``_ChunkedFieldReadFunction.backward``, same file 1020-1105).
 * :mod:`oracle.reference_path` — op-for-op torch restatement of the reference's CPU path
   (``assoc_scan`` / ``hierarchical_scan`` / ``reference_field_read``, same file 333-416) and of
   the Field mixer / block forward (1131-1221, 300-325). Also the timed CPU baseline.
@@ -124,6 +127,40 @@ def rms_norm_f64(x, weight, eps: float = 1e-6) -> np.ndarray:
         raise ValueError(f"weight must be [{x.shape[-1]}], got {w.shape}")
     ms = np.mean(x * x, axis=-1, keepdims=True)
     return x / np.sqrt(ms + eps) * w
+
+
+def scan_f64_autograd(raw, tr, ti, gamma, state_in=None):
+    """Differentiable float64 Field scan (torch complex128), for gradient checks.
+
+    raw [B,T,3C], tr/ti/gamma [C], state_in [B,2C] planar or None, all float64 torch tensors
+    (requires_grad as needed). Returns (read [B,T,4C], state_out [B,2C]). Same formulas as
+    ``reference_field_read`` (canon:392-416): inj = tanh + i tanh, v = 0.9 sigmoid,
+    a = (1-v) lam, b = gamma v inj, s_t = a_t s_{t-1} + b_t, disp = v lam s_{t-1}; the scan is a
+    recursive doubling with out-of-place shifts so that autograd differentiates every step.
+    """
+    import torch
+
+    c = tr.numel()
+    inj = torch.complex(torch.tanh(raw[..., :c]), torch.tanh(raw[..., c:2 * c]))
+    v = 0.9 * torch.sigmoid(raw[..., 2 * c:])
+    lam = torch.complex(tr, ti)
+    a = (1.0 - v) * lam
+    b = gamma * v * inj
+    b_len, t_len = raw.shape[0], raw.shape[1]
+    s0 = (torch.zeros((b_len, c), dtype=a.dtype) if state_in is None
+          else torch.complex(state_in[:, :c], state_in[:, c:]))
+    b = torch.cat((b[:, :1] + a[:, :1] * s0[:, None], b[:, 1:]), dim=1)
+    step = 1
+    while step < t_len:
+        a_prev = torch.cat((torch.ones_like(a[:, :step]), a[:, :-step]), dim=1)
+        b_prev = torch.cat((torch.zeros_like(b[:, :step]), b[:, :-step]), dim=1)
+        b = a * b_prev + b
+        a = a * a_prev
+        step *= 2
+    prev = torch.cat((s0[:, None], b[:, :-1]), dim=1)
+    disp = v * lam * prev
+    read = torch.cat((b.real, b.imag, disp.real, disp.imag), dim=-1)
+    return read, torch.cat((b[:, -1].real, b[:, -1].imag), dim=-1)
 
 
 def rel_err(actual, expected) -> float:

@@ -1,0 +1,208 @@
+"""GPU parity of the backward scan (fl_scan_backward; canon:1020-1105) against the gradients of
+the float64 oracle (torch autograd through ``oracle.scan_f64_autograd``, itself pinned by finite
+differences), and the autograd path of the Field modules.
+
+Tolerance: norm-wise relative error <= 1e-4 for grad_raw, the transition-parameter gradients and
+grad_state_in (fp32 adjoint against float64); the reference's own Triton-vs-reference bar is 2e-2
+(canon:1479-1488). bf16 grad_raw equals the fp32 one rounded to nearest even, bit for bit.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-4
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from fields_lm_amd import _native
+
+    _native.load()
+    return torch.device("cuda:0")
+
+
+def _params(C, seed):
+    rl, th = ref.init_radius_theta(C)
+    g = torch.Generator().manual_seed(seed)
+    rl = rl + 0.5 * torch.randn(C, generator=g)
+    th = th + 0.3 * torch.randn(C, generator=g)
+    return ref.transition_params(rl, th)
+
+
+def _oracle_grads(raw, tr, ti, gamma, grad_read, state_in=None, grad_state_out=None):
+    """float64 gradients of <grad_read, read> + <grad_state_out, state_out>."""
+    r = raw.double().clone().requires_grad_()
+    p = [t.double().clone().requires_grad_() for t in (tr, ti, gamma)]
+    s0 = None if state_in is None else state_in.double().clone().requires_grad_()
+    read, state = oracle.scan_f64_autograd(r, *p, s0)
+    loss = (read * grad_read.double()).sum()
+    if grad_state_out is not None:
+        loss = loss + (state * grad_state_out.double()).sum()
+    loss.backward()
+    return r.grad, p[0].grad, p[1].grad, p[2].grad, (None if s0 is None else s0.grad)
+
+
+SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
+          (4, 257, 512), (2, 1000, 1024), (1, 4099, 64)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_backward_matches_oracle_gradients(dev, shape, dtype):
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    B, T, C = shape
+    print(f"[case] backward shape={shape} dtype={dtype}", flush=True)
+    g = torch.Generator().manual_seed(B * 1000 + T + C + 7)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+    tr, ti, gamma = _params(C, seed=C + 1)
+    sin = torch.randn(B, 2 * C, generator=g) * 0.3
+    gread = torch.randn(B, T, 4 * C, generator=g)
+    gso = torch.randn(B, 2 * C, generator=g)
+    d = [t.to(dev) for t in (raw, tr, ti, gamma, sin, gread, gso)]
+    read, _ = field_scan(d[0], d[1], d[2], d[3], state_in=d[4], return_state=True)
+    g_raw, g_tr, g_ti, g_gm, g_sin = field_scan_backward(d[0], d[1], d[2], d[3], read, d[5], state_in=d[4],
+                                                         grad_state_out=d[6], return_state_grad=True)
+    torch.cuda.synchronize()
+    e_raw, e_tr, e_ti, e_gm, e_sin = _oracle_grads(raw.float(), tr, ti, gamma, gread, sin, gso)
+    assert g_raw.dtype == dtype
+    tol_raw = TOL if dtype == torch.float32 else 4e-3  # bf16 rounding of grad_raw: 2^-9 relative
+    assert oracle.rel_err(g_raw.float().cpu(), e_raw) <= tol_raw
+    assert oracle.rel_err(g_tr.cpu(), e_tr) <= TOL
+    assert oracle.rel_err(g_ti.cpu(), e_ti) <= TOL
+    assert oracle.rel_err(g_gm.cpu(), e_gm) <= TOL
+    assert oracle.rel_err(g_sin.cpu(), e_sin) <= TOL
+
+
+def test_backward_bf16_grad_is_rounded_fp32_grad(dev):
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan
+
+    print("[case] backward bf16 grad_raw", flush=True)
+    B, T, C = 3, 700, 512
+    g = torch.Generator().manual_seed(5)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, 5))
+    read = field_scan(raw, tr, ti, gamma)
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    lib = nat.load()
+    outs = {}
+    for gd in (torch.float32, torch.bfloat16):
+        gr = torch.empty(B, T, 3 * C, device=dev, dtype=gd)
+        gp = [torch.empty(C, device=dev) for _ in range(3)]
+        n = int(lib.fl_scan_backward_workspace_bytes(B, T, C))
+        ws = torch.zeros(n, device=dev, dtype=torch.uint8)
+        code = lib.fl_scan_backward(nat.ptr(raw), nat.FL_DTYPE_BF16, B, T, C, raw.stride(0), raw.stride(1),
+                                    nat.ptr(tr), nat.ptr(ti), nat.ptr(gamma), None, nat.ptr(read),
+                                    nat.ptr(gread), None, nat.ptr(gr), nat.dtype_code(gd), *[nat.ptr(x) for x in gp],
+                                    None, nat.ptr(ws), n, nat.stream_handle(dev))
+        nat.check(code, "fl_scan_backward")
+        torch.cuda.synchronize()
+        assert nat.workspace_error(ws) == 0
+        outs[gd] = (gr, gp)
+    torch.testing.assert_close(outs[torch.bfloat16][0], outs[torch.float32][0].to(torch.bfloat16), rtol=0, atol=0)
+    for a, b in zip(outs[torch.bfloat16][1], outs[torch.float32][1]):
+        torch.testing.assert_close(a, b, rtol=0, atol=0)
+
+
+def test_backward_is_linear_and_deterministic(dev):
+    """backward(g1 + 2 g2) = backward(g1) + 2 backward(g2) (the adjoint is linear), and repeated
+    calls give identical bits (fixed reduction order)."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    print("[case] backward linearity", flush=True)
+    B, T, C = 2, 900, 256
+    g = torch.Generator().manual_seed(6)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, 6))
+    read = field_scan(raw, tr, ti, gamma)
+    g1 = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    g2 = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    a = field_scan_backward(raw, tr, ti, gamma, read, g1)
+    b = field_scan_backward(raw, tr, ti, gamma, read, g2)
+    c = field_scan_backward(raw, tr, ti, gamma, read, g1 + 2 * g2)
+    c2 = field_scan_backward(raw, tr, ti, gamma, read, g1 + 2 * g2)
+    for x, y, z, z2 in zip(a, b, c, c2):
+        assert oracle.rel_err(z.cpu(), (x + 2 * y).cpu()) <= 1e-5
+        torch.testing.assert_close(z, z2, rtol=0, atol=0)
+
+
+def test_backward_full_size_config2_row(dev):
+    """Config 2 (B=8, T=2048, d=1024) at full size: batch row 3's grad_raw against the float64
+    oracle, and the parameter gradients against the sum of per-row oracle gradients of two rows
+    run alone (rows are independent)."""
+    from fields_lm_amd import field_scan, field_scan_backward
+    from fields_lm_amd.workloads import make_scan_workload
+
+    print("[case] backward config 2", flush=True)
+    wl = make_scan_workload("scan_b8_t2048_d1024", dev)
+    read = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma)
+    g = torch.Generator().manual_seed(8)
+    gread = torch.randn(read.shape, generator=g).to(dev)
+    g_raw, g_tr, _, _ = field_scan_backward(wl.raw, wl.tr, wl.ti, wl.gamma, read, gread)
+    row = 3
+    e_raw, _, _, _, _ = _oracle_grads(wl.raw[row:row + 1].float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu(),
+                                      gread[row:row + 1].cpu())
+    assert oracle.rel_err(g_raw[row:row + 1].float().cpu(), e_raw) <= 4e-3
+    rows = [field_scan_backward(wl.raw[r:r + 1], wl.tr, wl.ti, wl.gamma, read[r:r + 1].contiguous(),
+                                gread[r:r + 1].contiguous())[1] for r in range(8)]
+    assert oracle.rel_err(g_tr.cpu(), sum(x.double() for x in rows).cpu()) <= 1e-5
+
+
+def test_fused_field_read_autograd(dev):
+    """fused_field_read's backward (autograd) equals the oracle's gradients, through the
+    transition parameters' torch graph as well."""
+    from fields_lm_amd import fused_field_read
+
+    print("[case] fused_field_read autograd", flush=True)
+    B, T, C = 2, 150, 64
+    g = torch.Generator().manual_seed(9)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dev).requires_grad_()
+    tr, ti, gamma = (t.to(dev).requires_grad_() for t in _params(C, 9))
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    read = fused_field_read(raw, tr, ti, gamma, 32, 64)
+    (read * gread).sum().backward()
+    e_raw, e_tr, e_ti, e_gm, _ = _oracle_grads(raw.detach().cpu(), tr.detach().cpu(), ti.detach().cpu(),
+                                               gamma.detach().cpu(), gread.cpu())
+    assert oracle.rel_err(raw.grad.cpu(), e_raw) <= TOL
+    assert oracle.rel_err(tr.grad.cpu(), e_tr) <= TOL
+    assert oracle.rel_err(ti.grad.cpu(), e_ti) <= TOL
+    assert oracle.rel_err(gamma.grad.cpu(), e_gm) <= TOL
+
+
+def test_field_block_training_gradients(dev):
+    """A FieldBlock with gradients enabled takes the unfused path (fp32 read saved); its parameter
+    gradients equal those of a float64 CPU copy of the block whose scan is the oracle."""
+    from fields_lm_amd import FieldBlock
+
+    print("[case] FieldBlock gradients", flush=True)
+    torch.manual_seed(10)
+    block = FieldBlock(64, "triton", 32, 32, 64, 128)
+    x = torch.randn(2, 40, 64)
+    w = torch.randn(2, 40, 64)
+    gblock = block.to(dev)
+    y = gblock(x.to(dev))
+    (y * w.to(dev)).sum().backward()
+    got = {k: p.grad.detach().cpu() for k, p in gblock.named_parameters()}
+
+    cpu = FieldBlock(64, "triton", 32, 32, 64, 128).double()
+    cpu.load_state_dict({k: v.detach().cpu().double() for k, v in gblock.state_dict().items()})
+    m = cpu.mixer
+    xd = x.double()
+    raw = m.write_proj(xd)
+    tr, ti, gamma = m.transition()
+    read, _ = oracle.scan_f64_autograd(raw, tr.double(), ti.double(), gamma.double())
+    out = m.out_proj(m.read_norm(read))
+    h = xd + out * torch.sigmoid(m.gate_proj(xd))
+    yd = h + cpu.ff(cpu.ff_norm(h))
+    (yd * w.double()).sum().backward()
+    for k, p in cpu.named_parameters():
+        assert oracle.rel_err(got[k], p.grad) <= 2e-4, k

@@ -129,6 +129,34 @@ def test_rms_norm_invariants():
     np.testing.assert_allclose(oracle.rms_norm_f64(x, np.ones(64), 1e12), x / 1e6, rtol=1e-9)
 
 
+def test_autograd_oracle_forward_equals_c_oracle():
+    g = torch.Generator().manual_seed(21)
+    B, T, C = 2, 45, 6
+    raw = torch.randn(B, T, 3 * C, generator=g, dtype=torch.float64) * 2
+    tr, ti, gamma = (t.double() for t in _params(C, seed=21))
+    s0 = torch.randn(B, 2 * C, generator=g, dtype=torch.float64) * 0.3
+    read, state = oracle.scan_f64_autograd(raw, tr, ti, gamma, s0)
+    exp_read, exp_state = oracle.scan_f64(raw, tr, ti, gamma, state_in=s0)
+    assert oracle.rel_err(read.detach(), exp_read) <= 1e-12
+    assert oracle.rel_err(state.detach(), exp_state) <= 1e-12
+
+
+def test_autograd_oracle_gradients_match_finite_differences():
+    """torch.autograd.gradcheck (central differences) pins the oracle's gradients with respect
+    to raw, the transition parameters and the initial state."""
+    g = torch.Generator().manual_seed(22)
+    B, T, C = 1, 7, 2
+    raw = (torch.randn(B, T, 3 * C, generator=g, dtype=torch.float64) * 1.5).requires_grad_()
+    tr, ti, gamma = (t.double().clone().requires_grad_() for t in _params(C, seed=22))
+    s0 = (torch.randn(B, 2 * C, generator=g, dtype=torch.float64) * 0.3).requires_grad_()
+
+    def f(raw, tr, ti, gamma, s0):
+        read, state = oracle.scan_f64_autograd(raw, tr, ti, gamma, s0)
+        return read, state
+
+    assert torch.autograd.gradcheck(f, (raw, tr, ti, gamma, s0), eps=1e-6, atol=1e-7, rtol=1e-6)
+
+
 # ---------------------------------------------------------------------------------------------
 # closed forms
 # ---------------------------------------------------------------------------------------------
