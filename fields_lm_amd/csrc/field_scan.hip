@@ -1412,25 +1412,57 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 }
 
 // Sum of the per-tile parameter-gradient partials over the batch rows and chunks of each
-// channel, in a fixed order: grad_tr/ti/gamma[c] (overwritten).
-__global__ __launch_bounds__(256) void fl_param_grad_reduce_kernel(
+// channel: grad_tr/ti/gamma[c] (overwritten). One block per channel tile: lane <-> channel,
+// wave w sums the partial rows w, w + W, ... with kReduceUnroll independent accumulators, then
+// the waves' sums are added in wave order, so the result does not depend on timing.
+constexpr int kReduceWaves = 16;
+constexpr int kReduceUnroll = 8;
+
+__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_reduce_kernel(
     const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT,
     float* __restrict__ grad_tr, float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
-  const int ctile = c / CT, x = c - ctile * CT;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-  for (int b = 0; b < B; ++b) {
-    const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks) * 3 * CT + x;
-    for (int k = 0; k < n_chunks; ++k) {
-      a0 += row[(size_t)k * 3 * CT];
-      a1 += row[(size_t)k * 3 * CT + CT];
-      a2 += row[(size_t)k * 3 * CT + 2 * CT];
+  __shared__ float s_acc[kReduceWaves][3][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int ctile = blockIdx.x / (CT / 64);
+  const int x = (blockIdx.x - ctile * (CT / 64)) * 64 + lane;  // channel within the tile
+  const int c = ctile * CT + x;
+  const int n_rows = B * n_chunks;
+  float acc[3][kReduceUnroll];
+#pragma unroll
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int u = 0; u < kReduceUnroll; ++u) acc[p][u] = 0.f;
+  if (c < C) {
+    for (int r0 = wave * kReduceUnroll; r0 < n_rows; r0 += kReduceWaves * kReduceUnroll) {
+#pragma unroll
+      for (int u = 0; u < kReduceUnroll; ++u) {
+        const int r = r0 + u;
+        if (r < n_rows) {
+          const int b = r / n_chunks, k = r - b * n_chunks;
+          const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks + k) * 3 * CT + x;
+          acc[0][u] += row[0];
+          acc[1][u] += row[CT];
+          acc[2][u] += row[2 * CT];
+        }
+      }
     }
   }
-  grad_tr[c] = a0;
-  grad_ti[c] = a1;
-  grad_gamma[c] = a2;
+#pragma unroll
+  for (int p = 0; p < 3; ++p) {
+    float t = 0.f;
+#pragma unroll
+    for (int u = 0; u < kReduceUnroll; ++u) t += acc[p][u];
+    s_acc[wave][p][lane] = t;
+  }
+  __syncthreads();
+  if (wave == 0 && c < C) {
+    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+    for (int w = 0; w < kReduceWaves; ++w) { t0 += s_acc[w][0][lane]; t1 += s_acc[w][1][lane]; t2 += s_acc[w][2][lane]; }
+    grad_tr[c] = t0;
+    grad_ti[c] = t1;
+    grad_gamma[c] = t2;
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1911,7 +1943,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
-  fl_param_grad_reduce_kernel<<<(unsigned)cdiv(C, 256), 256, 0, stream>>>(
+  fl_param_grad_reduce_kernel<<<(unsigned)(g.n_ctiles * (CT / 64)), kReduceWaves * 64, 0, stream>>>(
       pgrad, (int)B, (int)C, g.n_chunks, g.n_ctiles, CT, grad_tr, grad_ti, grad_gamma);
   return hip_status(hipGetLastError());
 }
