@@ -312,12 +312,22 @@ def test_module_fused_equals_unfused(dev):
     assert oracle.rel_err(out16.float().cpu(), ref16.float().cpu()) <= 2e-2
 
 
-def test_module_fused_forward_is_forward_only(dev):
+def test_module_path_follows_gradient_need(dev):
+    """Inference (no gradient) runs read_norm inside the scan; with gradients the mixer runs the
+    scan + the RMSNorm module (read_norm's hook fires) and backward works through fl_scan_backward."""
     from fields_lm_amd import IndependentVacancyField
 
-    print("[case] module fused backward raises", flush=True)
+    print("[case] module path vs gradient need", flush=True)
     mixer = IndependentVacancyField(64, "triton", 32, 32, 64).to(dev)
-    x = torch.randn(1, 10, 64, device=dev, requires_grad=True)
-    y = mixer(x)
-    with pytest.raises(NotImplementedError):
-        y.sum().backward()
+    calls = []
+    mixer.read_norm.register_forward_hook(lambda m, i, o: calls.append(1))
+    x = torch.randn(1, 10, 64, device=dev)
+    with torch.no_grad():
+        y0 = mixer(x)
+    assert not calls  # fused
+    y = mixer(x.requires_grad_())
+    assert calls  # unfused, differentiable
+    y.sum().backward()
+    assert x.grad is not None and torch.isfinite(x.grad).all()
+    assert mixer.radius_logit.grad is not None and mixer.theta.grad is not None
+    assert oracle.rel_err(y.detach().cpu(), y0.cpu()) <= 1e-5
