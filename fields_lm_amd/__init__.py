@@ -24,6 +24,8 @@ from .field import (  # noqa: F401
     field_scan,
     field_scan_backward,
     field_scan_norm,
+    gate_residual_norm,
+    swiglu,
     fused_field_read,
     state_to_complex,
 )

@@ -1673,6 +1673,99 @@ __global__ __launch_bounds__(kBoundaryWaves * 64) void fl_boundary_scan_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
+// Field block elementwise tail (canon:1193-1195, 1219-1221, RMSNorm 300-309, SwiGLU 312-325),
+// fused for the inference path. Each value is rounded exactly where the stock ops round it:
+// an op on bf16 tensors computes in fp32 and rounds its result to bf16.
+//   fl_gate_residual_norm:  gate = sigmoid(g), prod = out * gate (in the GEMM output dtype G),
+//                           x1 = x + prod (in the residual dtype X), h = RMSNorm(x1) * w (fp32
+//                           math, rounded to X) — one block per row, x1 kept in registers.
+//   fl_swiglu:              out = silu(gate) * up with [gate | up] = the packed GEMM output.
+// ------------------------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ float round_as(float v);
+template <>
+__device__ __forceinline__ float round_as<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float round_as<bf16_bits>(float v) { return __uint_as_float(bf16_bits_of(v) << 16); }
+
+template <typename T>
+__device__ __forceinline__ float load_as(const T* p);
+template <>
+__device__ __forceinline__ float load_as<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_as<bf16_bits>(const bf16_bits* p) { return __uint_as_float((uint32_t)*p << 16); }
+
+constexpr int kTailThreads = 256;
+
+template <typename XT, typename GT, int NPER>
+__global__ __launch_bounds__(kTailThreads) void fl_gate_residual_norm_kernel(
+    const XT* __restrict__ x, const GT* __restrict__ out, const GT* __restrict__ gpre, int dim,
+    const float* __restrict__ w, float eps, float inv_dim, XT* __restrict__ x_new,
+    XT* __restrict__ normed) {
+  __shared__ float s_red[kTailThreads / 64];
+  const int64_t base = (int64_t)blockIdx.x * dim;
+  auto residual = [&](int c) {
+    const float gate = round_as<GT>(1.0f / (1.0f + expf(-load_as<GT>(gpre + base + c))));
+    const float prod = round_as<GT>(load_as<GT>(out + base + c) * gate);
+    return round_as<XT>(load_as<XT>(x + base + c) + prod);
+  };
+  float v[NPER > 0 ? NPER : 1];
+  float acc = 0.f;
+  if constexpr (NPER > 0) {
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int c = threadIdx.x + i * kTailThreads;
+      v[i] = c < dim ? residual(c) : 0.f;
+      acc = fmaf(v[i], v[i], acc);
+    }
+  } else {
+    for (int c = threadIdx.x; c < dim; c += kTailThreads) {
+      const float r = residual(c);
+      acc = fmaf(r, r, acc);
+    }
+  }
+#pragma unroll
+  for (int m = 1; m < 64; m <<= 1) acc += __shfl_xor(acc, m);
+  if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kTailThreads / 64; ++i) tot += s_red[i];
+  const float scale = rsqrtf(fmaf(tot, inv_dim, eps));
+  if constexpr (NPER > 0) {
+#pragma unroll
+    for (int i = 0; i < NPER; ++i) {
+      const int c = threadIdx.x + i * kTailThreads;
+      if (c < dim) {
+        store_out(x_new + base + c, v[i]);
+        store_out(normed + base + c, (v[i] * scale) * w[c]);
+      }
+    }
+  } else {
+    for (int c = threadIdx.x; c < dim; c += kTailThreads) {
+      const float r = residual(c);
+      store_out(x_new + base + c, r);
+      store_out(normed + base + c, (r * scale) * w[c]);
+    }
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void fl_swiglu_kernel(const T* __restrict__ gu, int64_t rows,
+                                                        int hidden, T* __restrict__ out) {
+  const int64_t n = rows * hidden;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / hidden;
+    const int j = (int)(i - r * hidden);
+    const float g = load_as<T>(gu + r * 2 * hidden + j);
+    const float u = load_as<T>(gu + r * 2 * hidden + hidden + j);
+    const float sg = round_as<T>(g / (1.0f + expf(-g)));
+    store_out(out + i, sg * u);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------------
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -2166,6 +2259,61 @@ int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64
   if (g16) { FL_BW(float, bf16_bits) }
   FL_BW(float, float)
 #undef FL_BW
+}
+
+int fl_gate_residual_norm(const void* x, int x_dtype, const void* out, const void* gate_pre,
+                          int g_dtype, int64_t rows, int64_t dim, const float* norm_weight,
+                          float eps, void* x_new, void* normed, void* stream) {
+  if ((x_dtype != FL_DTYPE_F32 && x_dtype != FL_DTYPE_BF16) ||
+      (g_dtype != FL_DTYPE_F32 && g_dtype != FL_DTYPE_BF16))
+    return FL_ERR_DTYPE;
+  if (rows <= 0 || dim <= 0 || rows > ((int64_t)1 << 31) - 1 || dim > ((int64_t)1 << 24))
+    return FL_ERR_INVALID_ARGUMENT;
+  if (!x || !out || !gate_pre || !norm_weight || !x_new || !normed || !(eps >= 0.f))
+    return FL_ERR_INVALID_ARGUMENT;
+  const size_t xs = x_dtype == FL_DTYPE_BF16 ? 2 : 4, gs = g_dtype == FL_DTYPE_BF16 ? 2 : 4;
+  if (!aligned(x, xs) || !aligned(x_new, xs) || !aligned(normed, xs) || !aligned(out, gs) ||
+      !aligned(gate_pre, gs) || !aligned(norm_weight, 4))
+    return FL_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float inv = (float)(1.0 / (double)dim);
+#define FL_GRN1(X, G, N)                                                                        \
+  fl_gate_residual_norm_kernel<X, G, N><<<(unsigned)rows, kTailThreads, 0, s>>>(                \
+      static_cast<const X*>(x), static_cast<const G*>(out), static_cast<const G*>(gate_pre),    \
+      (int)dim, norm_weight, eps, inv, static_cast<X*>(x_new), static_cast<X*>(normed));        \
+  return hip_status(hipGetLastError());
+#define FL_GRN(X, G)                                                                            \
+  if (dim <= kTailThreads) { FL_GRN1(X, G, 1) }                                                 \
+  if (dim <= 2 * kTailThreads) { FL_GRN1(X, G, 2) }                                             \
+  if (dim <= 4 * kTailThreads) { FL_GRN1(X, G, 4) }                                             \
+  if (dim <= 8 * kTailThreads) { FL_GRN1(X, G, 8) }                                             \
+  FL_GRN1(X, G, 0)
+  const bool x16 = x_dtype == FL_DTYPE_BF16, g16 = g_dtype == FL_DTYPE_BF16;
+  if (x16 && g16) { FL_GRN(bf16_bits, bf16_bits) }
+  if (x16) { FL_GRN(bf16_bits, float) }
+  if (g16) { FL_GRN(float, bf16_bits) }
+  FL_GRN(float, float)
+#undef FL_GRN
+#undef FL_GRN1
+}
+
+int fl_swiglu(const void* gate_up, int dtype, int64_t rows, int64_t hidden, void* out,
+              void* stream) {
+  if (dtype != FL_DTYPE_F32 && dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
+  if (rows <= 0 || hidden <= 0 || hidden > ((int64_t)1 << 30)) return FL_ERR_INVALID_ARGUMENT;
+  if (!gate_up || !out) return FL_ERR_INVALID_ARGUMENT;
+  const size_t es = dtype == FL_DTYPE_BF16 ? 2 : 4;
+  if (!aligned(gate_up, es) || !aligned(out, es)) return FL_ERR_INVALID_ARGUMENT;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t n = rows * hidden;
+  const unsigned blocks = (unsigned)(cdiv(n, 256) < 4096 ? cdiv(n, 256) : 4096);
+  if (dtype == FL_DTYPE_BF16)
+    fl_swiglu_kernel<bf16_bits><<<blocks, 256, 0, s>>>(static_cast<const bf16_bits*>(gate_up), rows,
+                                                        (int)hidden, static_cast<bf16_bits*>(out));
+  else
+    fl_swiglu_kernel<float><<<blocks, 256, 0, s>>>(static_cast<const float*>(gate_up), rows,
+                                                    (int)hidden, static_cast<float*>(out));
+  return hip_status(hipGetLastError());
 }
 
 int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, int64_t R,

@@ -350,6 +350,52 @@ def boundary_scan(a: torch.Tensor, drive: torch.Tensor, state_in: Optional[torch
     return (out, sout) if return_state else out
 
 
+def gate_residual_norm(x: torch.Tensor, out: torch.Tensor, gate_pre: torch.Tensor,
+                       weight: torch.Tensor, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``x + out * sigmoid(gate_pre)`` and its RMSNorm (``fl_gate_residual_norm``): the mixer's
+    gated residual (canon:1193-1195) and the block's ``ff_norm`` (canon:1219-1221) in one launch,
+    rounded as the stock ops round. x: residual stream (fp32 / bf16); out, gate_pre: the out_proj /
+    gate_proj outputs; all [..., dim] on one device. Returns (x_new, normed) in x's dtype."""
+    lib = nat.load()
+    if not x.is_cuda:
+        raise RuntimeError("gate_residual_norm requires a ROCm (cuda) device")
+    if out.shape != x.shape or gate_pre.shape != x.shape or out.dtype != gate_pre.dtype:
+        raise ValueError("x, out and gate_pre must have one shape; out and gate_pre one dtype")
+    dim = x.shape[-1]
+    if weight.numel() != dim:
+        raise ValueError("weight must have dim entries")
+    x, out, gate_pre = x.contiguous(), out.contiguous(), gate_pre.contiguous()
+    w = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
+    x_new, normed = torch.empty_like(x), torch.empty_like(x)
+    rows = x.numel() // dim if dim else 0
+    if rows == 0:
+        return x_new, normed
+    code = lib.fl_gate_residual_norm(nat.ptr(x), nat.dtype_code(x.dtype), nat.ptr(out), nat.ptr(gate_pre),
+                                     nat.dtype_code(out.dtype), rows, dim, nat.ptr(w), ctypes.c_float(float(eps)),
+                                     nat.ptr(x_new), nat.ptr(normed), nat.stream_handle(x.device))
+    nat.check(code, "fl_gate_residual_norm")
+    return x_new, normed
+
+
+def swiglu(gate_up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up with [gate | up] = gate_up [..., 2H] (``fl_swiglu``; canon:323-325)."""
+    lib = nat.load()
+    if not gate_up.is_cuda:
+        raise RuntimeError("swiglu requires a ROCm (cuda) device")
+    if gate_up.shape[-1] % 2:
+        raise ValueError("the last dimension must be even")
+    gate_up = gate_up.contiguous()
+    hidden = gate_up.shape[-1] // 2
+    out = torch.empty((*gate_up.shape[:-1], hidden), device=gate_up.device, dtype=gate_up.dtype)
+    rows = gate_up.numel() // (2 * hidden) if hidden else 0
+    if rows == 0:
+        return out
+    code = lib.fl_swiglu(nat.ptr(gate_up), nat.dtype_code(gate_up.dtype), rows, hidden, nat.ptr(out),
+                         nat.stream_handle(gate_up.device))
+    nat.check(code, "fl_swiglu")
+    return out
+
+
 def state_to_complex(state: torch.Tensor) -> torch.Tensor:
     """Planar [B,2C] fp32 state -> complex64 [B,C]."""
     c = state.shape[-1] // 2
@@ -465,16 +511,31 @@ class IndependentVacancyField(nn.Module):
             return torch.bfloat16 if raw.dtype == torch.bfloat16 else torch.float32
         return self.read_dtype
 
-    def forward(self, x: torch.Tensor) -> torch.Tensor:
+    def normed_read(self, x: torch.Tensor) -> torch.Tensor:
+        """read_norm(read) of the scan of x: what out_proj consumes."""
         tr, ti, gamma = self.transition()
         raw = self._raw(x)
         if self._fused(x):
-            normed = _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
-                                                  self.read_norm.eps, self._read_dtype(raw))
-            return self._project(x, normed)
+            return _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
+                                                self.read_norm.eps, self._read_dtype(raw))
         read = fused_field_read(raw, tr, ti, gamma, self.triton_block_c, self.triton_chunk_t,
                                 read_dtype=self._read_dtype(raw))
-        return self._readout(x, read)
+        return self.read_norm(read)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self._project(x, self.normed_read(x))
+
+    def normed_prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
+                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+        """read_norm(read) over [B,T,dim] and the recurrent state s[T-1] (fp32 [B,2C])."""
+        tr, ti, gamma = self.transition()
+        raw = self._raw(x)
+        if self._fused(x):
+            return field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight, self.read_norm.eps,
+                                   state_in=state, return_state=True, out_dtype=self._read_dtype(raw))
+        read, new_state = field_scan(raw, tr, ti, gamma, state_in=state, return_state=True,
+                                     read_dtype=self._read_dtype(raw))
+        return self.read_norm(read), new_state
 
     def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
@@ -482,16 +543,8 @@ class IndependentVacancyField(nn.Module):
 
         ``state`` continues a previous segment (state_in); None starts from zero as forward does.
         """
-        tr, ti, gamma = self.transition()
-        raw = self._raw(x)
-        if self._fused(x):
-            normed, new_state = field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight,
-                                                self.read_norm.eps, state_in=state,
-                                                return_state=True, out_dtype=self._read_dtype(raw))
-            return self._project(x, normed), new_state
-        read, new_state = field_scan(raw, tr, ti, gamma, state_in=state, return_state=True,
-                                     read_dtype=self._read_dtype(raw))
-        return self._readout(x, read), new_state
+        normed, new_state = self.normed_prefill(x, state)
+        return self._project(x, normed), new_state
 
     def decode_params(self) -> Tuple[torch.Tensor, ...]:
         """(tr, ti, gamma, read_norm weight in fp32): what :meth:`step` reads, cached once per
@@ -505,16 +558,19 @@ class IndependentVacancyField(nn.Module):
         ``params`` = a cached ``self.transition()`` or ``self.decode_params()`` (recomputed when
         None).
         """
+        return self._project(x_t, self.normed_step(x_t, state, params))
+
+    def normed_step(self, x_t: torch.Tensor, state: torch.Tensor,
+                    params: Optional[Tuple[torch.Tensor, ...]] = None) -> torch.Tensor:
+        """read_norm(read_t) of one decode token; ``state`` advances in place."""
         params = params if params is not None else self.decode_params()
         tr, ti, gamma = params[:3]
         raw_t = self._raw(x_t)
         if self._fused(x_t):
             w = params[3] if len(params) > 3 else self.read_norm.weight.detach().float().contiguous()
-            normed = field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
-                                            out_dtype=self._read_dtype(raw_t))
-            return self._project(x_t, normed)
-        read_t = field_decode_step(raw_t, tr, ti, gamma, state)
-        return self._readout(x_t, read_t)
+            return field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
+                                          out_dtype=self._read_dtype(raw_t))
+        return self.read_norm(field_decode_step(raw_t, tr, ti, gamma, state))
 
     def new_state(self, batch: int, device=None) -> torch.Tensor:
         return torch.zeros((batch, 2 * self.channels), device=device, dtype=torch.float32)
@@ -529,17 +585,42 @@ class FieldBlock(nn.Module):
         self.mixer = IndependentVacancyField(dim, backend, field_chunk, triton_block_c, triton_chunk_t)
         self.ff_norm = RMSNorm(dim)
         self.ff = PackedSwiGLU(dim, hidden=ff_hidden)
+        # True: the elementwise tail runs fused (fl_gate_residual_norm, fl_swiglu) when no
+        # gradient is needed. Not a parameter or buffer: state_dict is unchanged.
+        self.fuse_tail = True
+
+    # The elementwise tail (gated residual, ff_norm, SwiGLU activation) runs in two fused launches
+    # on the inference path (no gradient needed); the GEMMs stay stock.
+    def _fused_tail(self, x: torch.Tensor) -> bool:
+        if not self.fuse_tail or type(self.ff_norm) is not RMSNorm:
+            return False
+        if not (hasattr(self.ff, "w12") or hasattr(self.ff, "gate_up")):
+            return False
+        return not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())))
+
+    def _tail(self, x: torch.Tensor, normed: torch.Tensor) -> torch.Tensor:
+        m = self.mixer
+        x1, h = gate_residual_norm(x, m.out_proj(normed), m.gate_proj(x), self.ff_norm.weight, self.ff_norm.eps)
+        first, second = (self.ff.w12, self.ff.w3) if hasattr(self.ff, "w12") else (self.ff.gate_up, self.ff.down)
+        return x1 + second(swiglu(first(h)))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self._fused_tail(x):
+            return self._tail(x, self.mixer.normed_read(x))
         x = self.mixer(x)
         return x + self.ff(self.ff_norm(x))
 
     def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
+        if self._fused_tail(x):
+            normed, state = self.mixer.normed_prefill(x, state)
+            return self._tail(x, normed), state
         x, state = self.mixer.prefill(x, state)
         return x + self.ff(self.ff_norm(x)), state
 
     def step(self, x_t: torch.Tensor, state: torch.Tensor, params=None) -> torch.Tensor:
+        if self._fused_tail(x_t):
+            return self._tail(x_t, self.mixer.normed_step(x_t, state, params))
         x_t = self.mixer.step(x_t, state, params)
         return x_t + self.ff(self.ff_norm(x_t))
 

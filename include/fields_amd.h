@@ -179,6 +179,26 @@ int fl_decode_norm_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C,
 int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, int64_t R,
                      const float* state_in, float* state_out, float* out, void* stream);
 
+/*
+ * Field block elementwise tail for inference, one launch per row block:
+ *   x_new  = x + out * sigmoid(gate_pre)            (IndependentVacancyField.forward return,
+ *                                                    field_only_v4_chunked_triton_wiki100.py:1193-1195)
+ *   normed = RMSNorm(x_new) * norm_weight           (FieldBlock.ff_norm, same file 1219-1221, 300-309)
+ * out / gate_pre are the out_proj / gate_proj GEMM outputs (g_dtype), x / x_new / normed the
+ * residual stream (x_dtype); all [rows, dim] contiguous. Every intermediate is rounded where the
+ * stock ops round it (bf16 ops compute in fp32 and round their result).
+ */
+int fl_gate_residual_norm(const void* x, int x_dtype, const void* out, const void* gate_pre,
+                          int g_dtype, int64_t rows, int64_t dim, const float* norm_weight,
+                          float eps, void* x_new, void* normed, void* stream);
+
+/*
+ * SwiGLU activation of the Field block FFN (PackedSwiGLU.forward, same file 312-325):
+ * out[r, j] = silu(gate_up[r, j]) * gate_up[r, hidden + j], [rows, 2*hidden] -> [rows, hidden].
+ */
+int fl_swiglu(const void* gate_up, int dtype, int64_t rows, int64_t hidden, void* out,
+              void* stream);
+
 /* Library version string (host function). No counterpart in the reference. */
 const char* fl_version(void);
 

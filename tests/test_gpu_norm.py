@@ -331,3 +331,86 @@ def test_module_path_follows_gradient_need(dev):
     assert x.grad is not None and torch.isfinite(x.grad).all()
     assert mixer.radius_logit.grad is not None and mixer.theta.grad is not None
     assert oracle.rel_err(y.detach().cpu(), y0.cpu()) <= 1e-5
+
+
+# ---------------------------------------------------------------------------------------------
+# fused elementwise tail of the Field block (fl_gate_residual_norm, fl_swiglu)
+# ---------------------------------------------------------------------------------------------
+
+def _close_to_stock(got, exp, scale):
+    """Every element within one bf16 step of the stock result (an fp32 sigmoid / exp may differ
+    from the stock one in its last bit and flip a bf16 rounding; ``scale`` bounds the magnitude of
+    the rounded intermediate), and >= 99 % of them within 1e-5 relative (sums in another order)."""
+    got, exp, scale = got.float(), exp.float(), scale.float().abs()
+    diff = (got - exp).abs()
+    assert bool((diff <= 2.0 ** -7 * (exp.abs() + scale) + 1e-6).all()), float(diff.max())
+    assert float((diff <= 1e-5 * exp.abs() + 1e-7).float().mean()) >= 0.99
+
+
+@pytest.mark.parametrize("xd,gd", [(torch.bfloat16, torch.bfloat16), (torch.float32, torch.bfloat16),
+                                   (torch.float32, torch.float32)], ids=["bf16", "f32_bf16", "f32"])
+@pytest.mark.parametrize("rows,dim", [(64, 1024), (3, 2048), (5, 100), (2, 3000), (1, 1)])
+def test_gate_residual_norm_matches_stock_ops(dev, xd, gd, rows, dim):
+    from fields_lm_amd import RMSNorm, gate_residual_norm
+
+    print(f"[case] gate_residual_norm {xd} {gd} {rows}x{dim}", flush=True)
+    g = torch.Generator().manual_seed(rows * 7 + dim)
+    x = torch.randn(rows, dim, generator=g).to(xd).to(dev)
+    out = torch.randn(rows, dim, generator=g).to(gd).to(dev)
+    gp = (torch.randn(rows, dim, generator=g) * 2).to(gd).to(dev)
+    norm = RMSNorm(dim).to(dev)
+    with torch.no_grad():
+        norm.weight.copy_(1.0 + 0.3 * torch.randn(dim, generator=g))
+        exp_x = x + (out * torch.sigmoid(gp)).to(x.dtype)   # canon:1193-1195
+        exp_h = norm(exp_x)                                   # canon:300-309
+    x1, h = gate_residual_norm(x, out, gp, norm.weight, norm.eps)
+    assert x1.dtype == xd and h.dtype == xd
+    _close_to_stock(x1, exp_x, out)
+    _close_to_stock(h, exp_h, out * h.float() / exp_x.float().abs().clamp_min(1e-6))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_swiglu_matches_stock_ops(dev, dtype):
+    from fields_lm_amd import swiglu
+
+    print(f"[case] swiglu {dtype}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    for shape in [(64, 2 * 2528), (2, 7, 2 * 96), (1, 2)]:
+        gu = (torch.randn(*shape, generator=g) * 3).to(dtype).to(dev)
+        gate, up = gu.chunk(2, dim=-1)
+        exp = torch.nn.functional.silu(gate) * up             # canon:323-325
+        _close_to_stock(swiglu(gu), exp, up)
+
+
+def test_field_block_fused_tail_equals_stock_ops(dev):
+    from fields_lm_amd import FieldBlock
+    from fields_lm_amd.model import GateUpSwiGLU
+
+    print("[case] FieldBlock fused tail", flush=True)
+    torch.manual_seed(31)
+    block = FieldBlock(256, "triton", 32, 32, 64, 512).to(dev)
+    x = torch.randn(2, 70, 256, device=dev)
+    with torch.no_grad():
+        block.fuse_tail = False
+        ref32 = block(x)
+        y_ref, s_ref = block.prefill(x[:, :50])
+        block.fuse_tail = True
+        got32 = block(x)
+        y, s = block.prefill(x[:, :50])
+        params = block.mixer.decode_params()
+        steps = [block.step(x[:, t], s, params) for t in range(50, 70)]
+        block.ff = GateUpSwiGLU(256, 384).to(dev)  # the R1-resized FFN layout
+        block.fuse_tail = False
+        ref_gu = block(x)
+        block.fuse_tail = True
+        got_gu = block(x)
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            block.fuse_tail = False
+            ref16 = block(x)
+            block.fuse_tail = True
+            got16 = block(x)
+    assert oracle.rel_err(got32.cpu(), ref32.cpu()) <= 1e-5
+    assert oracle.rel_err(y.cpu(), y_ref.cpu()) <= 1e-5
+    assert oracle.rel_err(torch.stack(steps, 1).cpu(), ref32[:, 50:].cpu()) <= 1e-4
+    assert oracle.rel_err(got_gu.cpu(), ref_gu.cpu()) <= 1e-5
+    assert oracle.rel_err(got16.float().cpu(), ref16.float().cpu()) <= 2e-2
