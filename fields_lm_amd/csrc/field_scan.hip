@@ -1317,41 +1317,53 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], car[k], cai[k]);
       }
     }
+    // every load of the pass first (z_r, z_i, and s_{t-1} from the forward's read), then the
+    // dependent chain: no step waits on memory. Rows past T read as 0 through the descriptor
+    // bounds; the row before the sequence start reads 0 (out-of-range offset) and is replaced by
+    // state_in.
+    float zr[L][K], zi[L][K], pr[L][K], pi[L][K];
+    {
+      const bool first = t_begin == 0;
+      const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + (first ? 0 : t_begin - 1)) * 4 * C,
+                                      (uint32_t)((int64_t)(first ? rows : rows + 1) * 4 * C * 4));
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi[j]);
+        const int prow = wave * L + j - (first ? 1 : 0);
+        const int so = prow >= 0 ? prow * grd_row : 0x7fffffff;
+        RawLoad<float, K>::run(r_prev, vo_f, so, pr[j]);
+        RawLoad<float, K>::run(r_prev, vo_f, so == 0x7fffffff ? so : so + f_plane, pi[j]);
+      }
+      if (w0 == 0) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          pr[0][k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
+          pi[0][k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
+        }
+      }
+    }
 #pragma unroll
     for (int j = L - 1; j >= 0; --j) {
       if (j < n_valid) {
-        const int t = w0 + j;
-        float zr[K], zi[K], pr[K], pi[K];
-        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr);
-        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi);
-        if (t > 0) {
-          const float* prow = read + ((int64_t)b * T + t - 1) * 4 * C + c0;
-#pragma unroll
-          for (int k = 0; k < K; ++k) { pr[k] = ok ? prow[k] : 0.f; pi[k] = ok ? prow[C + k] : 0.f; }
-        } else {
-#pragma unroll
-          for (int k = 0; k < K; ++k) {
-            pr[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
-            pi[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
-          }
-        }
         float ozr[K], ozi[K], ozv[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           const float v = gv[j][k], keep = 1.f - v;
-          const float ur = __builtin_amdgcn_exp2f(fabsf(zr[k]) * (-2.0f * kLog2e));
-          const float ui = __builtin_amdgcn_exp2f(fabsf(zi[k]) * (-2.0f * kLog2e));
+          const float ur = __builtin_amdgcn_exp2f(fabsf(zr[j][k]) * (-2.0f * kLog2e));
+          const float ui = __builtin_amdgcn_exp2f(fabsf(zi[j][k]) * (-2.0f * kLog2e));
           const float er = 1.0f + ur, ei = 1.0f + ui;
           const float rdi = __builtin_amdgcn_rcpf(er * ei);
-          const float injr = copysignf((1.0f - ur) * (ei * rdi), zr[k]);
-          const float inji = copysignf((1.0f - ui) * (er * rdi), zi[k]);
+          const float injr = copysignf((1.0f - ur) * (ei * rdi), zr[j][k]);
+          const float inji = copysignf((1.0f - ui) * (er * rdi), zi[j][k]);
           const float Gr = uR[j][k] + car[k], Gi = uI[j][k] + cai[k];
-          const float mr = lr[k] * pr[k] - li[k] * pi[k];     // lam p
-          const float mi = lr[k] * pi[k] + li[k] * pr[k];
-          const float cb = injr * Gr + inji * Gi;             // Re(conj(G) inj)
+          const float p_r = pr[j][k], p_i = pi[j][k];
+          const float mr = lr[k] * p_r - li[k] * p_i;     // lam p
+          const float mi = lr[k] * p_i + li[k] * p_r;
+          const float cb = injr * Gr + inji * Gi;         // Re(conj(G) inj)
           const float dv = (dR[j][k] * mr + dI[j][k] * mi) - (Gr * mr + Gi * mi) + gm[k] * cb;
-          gtr[k] += keep * (Gr * pr[k] + Gi * pi[k]) + v * (dR[j][k] * pr[k] + dI[j][k] * pi[k]);
-          gti[k] += keep * (Gi * pr[k] - Gr * pi[k]) + v * (dI[j][k] * pr[k] - dR[j][k] * pi[k]);
+          gtr[k] += keep * (Gr * p_r + Gi * p_i) + v * (dR[j][k] * p_r + dI[j][k] * p_i);
+          gti[k] += keep * (Gi * p_r - Gr * p_i) + v * (dI[j][k] * p_r - dR[j][k] * p_i);
           ggm[k] += v * cb;
           const float gvv = gm[k] * v;
           ozr[k] = gvv * Gr * (1.0f - injr * injr);
