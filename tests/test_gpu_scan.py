@@ -423,3 +423,33 @@ def test_block_causality(dev):
         full = block(x)
         pre = block(x[:, :23].contiguous())
     assert float((full[:, :23] - pre).abs().max()) <= 2e-4
+
+
+@pytest.mark.parametrize("shape", [(1, 3, 65536), (65535, 2, 4), (7, 1, 3)], ids=["maxC", "maxB", "T1"])
+def test_limits_scan_decode_backward(dev, shape):
+    """The ABI's maximum channel count (65,536) and batch (65,535), and T = 1: forward (both
+    algorithms), decode steps and backward against the float64 oracle."""
+    from fields_lm_amd import field_decode_step, field_scan, field_scan_backward
+
+    B, T, C = shape
+    print(f"[case] limits {shape}", flush=True)
+    g = torch.Generator().manual_seed(B + T + C)
+    raw = torch.randn(B, T, 3 * C, generator=g) * 2
+    tr, ti, gamma = _params(C, seed=C)
+    draw, dtr, dti, dgm = _to(dev, raw, tr, ti, gamma)
+    exp_read, exp_state = oracle.scan_f64(raw, tr, ti, gamma)
+    for algo in ALGOS.values():
+        read, state = field_scan(draw, dtr, dti, dgm, return_state=True, algo=algo)
+        assert oracle.rel_err(read.cpu(), exp_read) <= TOL, algo
+        assert oracle.rel_err(state.cpu(), exp_state) <= TOL, algo
+    st = torch.zeros(B, 2 * C, device=dev)
+    rows = torch.stack([field_decode_step(draw[:, t].contiguous(), dtr, dti, dgm, st) for t in range(T)], 1)
+    assert oracle.rel_err(rows.cpu(), exp_read) <= TOL
+    gread = torch.randn(B, T, 4 * C, generator=g)
+    g_raw, g_tr, _, _ = field_scan_backward(draw, dtr, dti, dgm, read, gread.to(dev))
+    r = raw.double().requires_grad_()
+    p = [t.double().requires_grad_() for t in (tr, ti, gamma)]
+    out, _ = oracle.scan_f64_autograd(r, *p)
+    (out * gread.double()).sum().backward()
+    assert oracle.rel_err(g_raw.cpu(), r.grad) <= TOL
+    assert oracle.rel_err(g_tr.cpu(), p[0].grad) <= TOL
