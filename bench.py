@@ -507,7 +507,7 @@ def main() -> int:
     ap.add_argument("--decode-only", action="store_true",
                     help="only the B=64 decode comparison (kernel and block step in HIP graphs)")
     ap.add_argument("--backward-only", action="store_true",
-                    help="only the backward scan at config 2 (and config 4)")
+                    help="only the backward scan (fl_scan_backward) on --workload")
     ap.add_argument("--model", choices=["prefill", "decode"],
                     help="only the whole-model run: prefill (config 3) or decode (config 5)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -538,8 +538,8 @@ def main() -> int:
         print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
         return 0
     if args.backward_only:
-        print(json.dumps({"backward": [backward_timing("scan_b8_t2048_d1024"),
-                                       backward_timing("scan_b1_t65536_d1024", steps=20, warmup=3)]}), flush=True)
+        print(json.dumps({"backward": backward_timing(args.workload, steps=args.steps, warmup=args.warmup)}),
+              flush=True)
         return 0
     if args.model:
         fn = model_prefill if args.model == "prefill" else model_decode

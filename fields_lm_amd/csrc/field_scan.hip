@@ -1424,15 +1424,16 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 }
 
 // Sum of the per-tile parameter-gradient partials over the batch rows and chunks of each
-// channel: grad_tr/ti/gamma[c] (overwritten). One block per channel tile: lane <-> channel,
-// wave w sums the partial rows w, w + W, ... with kReduceUnroll independent accumulators, then
-// the waves' sums are added in wave order, so the result does not depend on timing.
-constexpr int kReduceWaves = 16;
-constexpr int kReduceUnroll = 8;
+// channel, in two deterministic stages: fl_param_grad_segment_kernel adds the partial rows of
+// one segment of (at least kReduceSegRows) rows for 64 channels (waves over interleaved rows, then the
+// waves in order), fl_param_grad_final_kernel adds the segments in order into grad_tr/ti/gamma
+// (overwritten). Many segments keep the whole chip busy when B * n_chunks is large.
+constexpr int kReduceWaves = 4;
+constexpr int kReduceSegRows = 32;
 
-__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_reduce_kernel(
-    const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT,
-    float* __restrict__ grad_tr, float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
+__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_segment_kernel(
+    const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT, int seg_rows,
+    float* __restrict__ seg) {
   __shared__ float s_acc[kReduceWaves][3][64];
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -1440,41 +1441,48 @@ __global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_reduce_kernel
   const int x = (blockIdx.x - ctile * (CT / 64)) * 64 + lane;  // channel within the tile
   const int c = ctile * CT + x;
   const int n_rows = B * n_chunks;
-  float acc[3][kReduceUnroll];
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
-#pragma unroll
-    for (int u = 0; u < kReduceUnroll; ++u) acc[p][u] = 0.f;
+  const int r_begin = blockIdx.y * seg_rows;
+  const int r_end = min(r_begin + seg_rows, n_rows);
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
   if (c < C) {
-    for (int r0 = wave * kReduceUnroll; r0 < n_rows; r0 += kReduceWaves * kReduceUnroll) {
-#pragma unroll
-      for (int u = 0; u < kReduceUnroll; ++u) {
-        const int r = r0 + u;
-        if (r < n_rows) {
-          const int b = r / n_chunks, k = r - b * n_chunks;
-          const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks + k) * 3 * CT + x;
-          acc[0][u] += row[0];
-          acc[1][u] += row[CT];
-          acc[2][u] += row[2 * CT];
-        }
-      }
+#pragma unroll 4
+    for (int r = r_begin + wave; r < r_end; r += kReduceWaves) {
+      const int b = r / n_chunks, k = r - b * n_chunks;
+      const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks + k) * 3 * CT + x;
+      a0 += row[0];
+      a1 += row[CT];
+      a2 += row[2 * CT];
     }
   }
-#pragma unroll
-  for (int p = 0; p < 3; ++p) {
-    float t = 0.f;
-#pragma unroll
-    for (int u = 0; u < kReduceUnroll; ++u) t += acc[p][u];
-    s_acc[wave][p][lane] = t;
-  }
+  s_acc[wave][0][lane] = a0;
+  s_acc[wave][1][lane] = a1;
+  s_acc[wave][2][lane] = a2;
   __syncthreads();
   if (wave == 0 && c < C) {
     float t0 = 0.f, t1 = 0.f, t2 = 0.f;
     for (int w = 0; w < kReduceWaves; ++w) { t0 += s_acc[w][0][lane]; t1 += s_acc[w][1][lane]; t2 += s_acc[w][2][lane]; }
-    grad_tr[c] = t0;
-    grad_ti[c] = t1;
-    grad_gamma[c] = t2;
+    float* out = seg + (size_t)blockIdx.y * 3 * C + c;
+    out[0] = t0;
+    out[C] = t1;
+    out[2 * C] = t2;
   }
+}
+
+__global__ __launch_bounds__(256) void fl_param_grad_final_kernel(
+    const float* __restrict__ seg, int n_seg, int C, float* __restrict__ grad_tr,
+    float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= C) return;
+  float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+  for (int i = 0; i < n_seg; ++i) {
+    const float* p = seg + (size_t)i * 3 * C + c;
+    t0 += p[0];
+    t1 += p[C];
+    t2 += p[2 * C];
+  }
+  grad_tr[c] = t0;
+  grad_ti[c] = t1;
+  grad_gamma[c] = t2;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2012,7 +2020,8 @@ constexpr LookbackTiling kBwdTiling = {1, 8, 8, 4};
 
 struct BwdLayout {
   LookbackGeom g;
-  size_t status_off, data_off, pgrad_off, bytes;
+  int n_seg, seg_rows;  // segments of the reduction (at most 65,535) and rows per segment
+  size_t status_off, data_off, pgrad_off, seg_off, bytes;
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
@@ -2022,7 +2031,11 @@ BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
   w.status_off = kHeaderBytes;
   w.data_off = w.status_off + (size_t)cdiv((int64_t)w.g.n_tiles * 4, 256) * 256;
   w.pgrad_off = w.data_off + (size_t)cdiv((int64_t)w.g.n_tiles * kPlanes * CT * 8, 256) * 256;
-  w.bytes = w.pgrad_off + (size_t)w.g.n_tiles * 3 * CT * sizeof(float);
+  const int64_t n_rows = B * (int64_t)w.g.n_chunks;
+  w.seg_rows = (int)(cdiv(n_rows, kReduceSegRows) <= 65535 ? kReduceSegRows : cdiv(n_rows, 65535));
+  w.n_seg = (int)cdiv(n_rows, w.seg_rows);
+  w.seg_off = w.pgrad_off + (size_t)cdiv((int64_t)w.g.n_tiles * 3 * CT * 4, 256) * 256;
+  w.bytes = w.seg_off + (size_t)w.n_seg * 3 * C * sizeof(float);
   return w;
 }
 
@@ -2048,8 +2061,14 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
-  fl_param_grad_reduce_kernel<<<(unsigned)(g.n_ctiles * (CT / 64)), kReduceWaves * 64, 0, stream>>>(
-      pgrad, (int)B, (int)C, g.n_chunks, g.n_ctiles, CT, grad_tr, grad_ti, grad_gamma);
+  float* seg = reinterpret_cast<float*>(ws + lay.seg_off);
+  fl_param_grad_segment_kernel<<<dim3((unsigned)(g.n_ctiles * (CT / 64)), (unsigned)lay.n_seg),
+                                 kReduceWaves * 64, 0, stream>>>(pgrad, (int)B, (int)C, g.n_chunks,
+                                                                 g.n_ctiles, CT, lay.seg_rows, seg);
+  e = hipGetLastError();
+  if (e != hipSuccess) return hip_status(e);
+  fl_param_grad_final_kernel<<<(unsigned)cdiv(C, 256), 256, 0, stream>>>(seg, lay.n_seg, (int)C, grad_tr,
+                                                                        grad_ti, grad_gamma);
   return hip_status(hipGetLastError());
 }
 
