@@ -1044,30 +1044,43 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       const int row = lane & (L - 1);
       const uint32_t tag_sib = ((epoch & 0x3fffffffu) << 2) | kTagSib;
       if (lane < L && row < n_valid) put_word(sib + (size_t)ticket * TC + wave * L + row, part, tag_sib);
+      // the norm weights are needed only after the exchange: load them now, under its wait
+      float nw[4][K];
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int k = 0; k < K; ++k) nw[p][k] = ok ? norm_w[p * C + c0 + k] : 0.f;
       // row totals over the group's channel tiles, summed in the same order by every tile
       float tot = 0.f;
       bool sib_failed = false;
       if (row < n_valid) {
         uint64_t* sg = sib + ((size_t)chunk * n_chains + (size_t)b * n_ctiles) * TC + wave * L + row;
         uint32_t spins = 0;
-        for (int s = lane / L; s < n_ctiles; s += 64 / L) {
-          uint64_t w = get_word(sg + (size_t)s * TC);
-          if (!settle_words<1>(sg + (size_t)s * TC, 0, tag_sib, &w, spins)) {
-            sib_failed = true;
-            break;
+        constexpr int kStride = 64 / L, kBatch = 4;  // lanes per row; words in flight per lane
+        for (int s0 = lane / L; s0 < n_ctiles && !sib_failed; s0 += kBatch * kStride) {
+          uint64_t w[kBatch];
+#pragma unroll
+          for (int q = 0; q < kBatch; ++q) {
+            const int sq = s0 + q * kStride;
+            w[q] = sq < n_ctiles ? get_word(sg + (size_t)sq * TC) : 0ull;
           }
-          tot += word_value(w);
+#pragma unroll
+          for (int q = 0; q < kBatch; ++q) {
+            const int sq = s0 + q * kStride;
+            if (sq < n_ctiles && !sib_failed) {
+              if (!settle_words<1>(sg + (size_t)sq * TC, 0, tag_sib, &w[q], spins)) {
+                sib_failed = true;
+              } else {
+                tot += word_value(w[q]);
+              }
+            }
+          }
         }
       }
 #pragma unroll
       for (int m = L; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
       if (__ballot(sib_failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
       const float scale = rsqrtf(fmaf(tot, inv_n, eps));
-      float nw[4][K];
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int k = 0; k < K; ++k) nw[p][k] = ok ? norm_w[p * C + c0 + k] : 0.f;
       tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
                                            io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
                                            si, scale, nw);
