@@ -61,6 +61,9 @@ VARIANTS = {  # name -> (ScanPlan keyword arguments, read bytes per element, pro
 }
 
 
+ALGOS = {"auto": 0, "lookback": 2, "chunked3": 1}  # fl_scan_forward_ex algo codes
+
+
 def measured_traffic(workload: str, variant: str = "read_fp32"):
     """HBM bytes per launch of the scan from the committed rocprofv3 --pmc summary, or None."""
     path = REPO / "profiles" / f"fl_scan_lookback_kernel_{workload}{VARIANTS[variant][2]}_pmc.txt"
@@ -504,6 +507,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="scan_b8_t2048_d1024")
     ap.add_argument("--variant", default="read_fp32", choices=list(VARIANTS))
+    ap.add_argument("--algo", default="auto", choices=list(ALGOS),
+                    help="scan algorithm of the timed step (auto: the library's default)")
     ap.add_argument("--decode-only", action="store_true",
                     help="only the B=64 decode comparison (kernel and block step in HIP graphs)")
     ap.add_argument("--backward-only", action="store_true",
@@ -553,6 +558,8 @@ def main() -> int:
         kw["read_dtype"] = torch.bfloat16
     if vkw.get("norm"):
         kw["norm_weight"] = torch.ones(4 * wl.channels, device=dev)  # read_norm's init weight
+    if not vkw.get("norm"):
+        kw["algo"] = ALGOS[args.algo]
     plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
     wall_ms, ev_ms = time_plan(plan, args.steps, args.warmup)
     bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype, read_bytes)
@@ -575,7 +582,7 @@ def main() -> int:
         "dtype": "fp32",
         "data": "synthetic",
         "config": {
-            "workload": args.workload, "variant": args.variant,
+            "workload": args.workload, "variant": args.variant, "algo": args.algo,
             "B": wl.raw.shape[0], "T": wl.raw.shape[1], "d_model": 2 * wl.channels,
             "raw_dtype": "bf16", "read_dtype": "fp32" if read_bytes == 4 else "bf16",
             "state_dtype": "fp32", "read_norm_fused": bool(vkw.get("norm")),

@@ -215,24 +215,25 @@ struct Store<4> {
 
 // ------------------------------------------------------------------------------------------
 // gates (canon:399-406; the Triton form canon:487-505, 599-615)
-//   inj = tanh(zr) + i tanh(zi),   v = 0.9 * sigmoid(zv),   b = gamma * v * inj
-// tanh(x) = sign(x) (1-u)/(1+u) with u = e^{-2|x|} in (0,1]: both denominators lie in [1,2],
-// so one v_rcp_f32 of their product serves both. sigmoid(z) = 1/(1+e^{-z}) with its own
-// v_rcp_f32 (rcp(inf) = 0 gives sigmoid(-inf) = 0). No clamps; NaN propagates.
-// exp is v_exp_f32 (2^x) on pre-scaled arguments.
+//   inj = tanh(zr) + i tanh(zi),   v = 0.9 * sigmoid(zv),   b = gamma * v * inj,
+// returned as keep = 1 - v and b. With scale = gamma * v (g9 = 0.9 * gamma per channel):
+//   b_r = scale * tanh(zr) = scale - 2 scale / (1 + e^{2 zr})   (one fma after the reciprocal),
+//   sigmoid(z) = 1 / (1 + e^{-z}),   keep = 1 - 0.9 sigmoid(zv)   (one fma),
+// so a channel-step costs 3 v_exp_f32 (2^x on pre-scaled arguments), 3 v_rcp_f32 and 8
+// full-rate ops. Every limit is exact without clamps: e^{2x} = inf gives tanh = 1, e^{2x} = 0
+// gives tanh = -1, rcp(inf) = 0 gives sigmoid(-inf) = 0; NaN propagates. Near x = 0 the form
+// 1 - 2/(1+e^{2x}) carries an absolute error of a few fp32 ulps of 1 (not relative to tanh x).
 // ------------------------------------------------------------------------------------------
-__device__ __forceinline__ void gates(float zr, float zi, float zv, float gm, float& v,
+__device__ __forceinline__ void gates(float zr, float zi, float zv, float g9, float& keep,
                                       float& br, float& bi) {
-  const float ur = __builtin_amdgcn_exp2f(fabsf(zr) * (-2.0f * kLog2e));
-  const float ui = __builtin_amdgcn_exp2f(fabsf(zi) * (-2.0f * kLog2e));
-  const float dr = 1.0f + ur, di = 1.0f + ui;
-  const float rdi = __builtin_amdgcn_rcpf(dr * di);
-  const float tr_abs = (1.0f - ur) * (di * rdi);
-  const float ti_abs = (1.0f - ui) * (dr * rdi);
-  v = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv * -kLog2e));
-  const float scale = gm * v;
-  br = scale * copysignf(tr_abs, zr);
-  bi = scale * copysignf(ti_abs, zi);
+  const float er = __builtin_amdgcn_exp2f(zr * (2.0f * kLog2e));
+  const float ei = __builtin_amdgcn_exp2f(zi * (2.0f * kLog2e));
+  const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv * -kLog2e));
+  const float scale = g9 * sg;
+  const float m2 = -2.0f * scale;
+  br = fmaf(m2, __builtin_amdgcn_rcpf(1.0f + er), scale);
+  bi = fmaf(m2, __builtin_amdgcn_rcpf(1.0f + ei), scale);
+  keep = fmaf(-kVacancyMax, sg, 1.0f);
 }
 
 // complex power lam^n by repeated squaring (n >= 0)
@@ -266,13 +267,16 @@ __device__ __forceinline__ void apply_map(float lnr, float lni, float P, float B
 // ------------------------------------------------------------------------------------------
 template <typename RawT, int K, int L>
 struct WaveTile {
-  float gv[L][K], gbr[L][K], gbi[L][K];  // gates, kept between summary and materialisation
+  // gates, kept between summary and materialisation: keep = 1 - v, b
+  float gk[L][K], gbr[L][K], gbi[L][K];
 
   // Loads L rows from the raw descriptor (row j at soffset so0 + j*row_bytes) and forms gates.
   // Rows past the descriptor's bound read as 0; their gates are never used.
   __device__ __forceinline__ void load(rsrc_t r, int vo, int so0, int row_bytes, int plane_bytes,
                                        const float* gm) {
-    float z[L][3][K];
+    float z[L][3][K], g9[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) g9[k] = kVacancyMax * gm[k];
 #pragma unroll
     for (int j = 0; j < L; ++j) {
       const int so = so0 + j * row_bytes;
@@ -284,7 +288,7 @@ struct WaveTile {
     for (int j = 0; j < L; ++j) {
 #pragma unroll
       for (int k = 0; k < K; ++k)
-        gates(z[j][0][k], z[j][1][k], z[j][2][k], gm[k], gv[j][k], gbr[j][k], gbi[j][k]);
+        gates(z[j][0][k], z[j][1][k], z[j][2][k], g9[k], gk[j][k], gbr[j][k], gbi[j][k]);
     }
   }
 
@@ -297,7 +301,7 @@ struct WaveTile {
     for (int j = 0; j < L; ++j) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
-        const float keep = 1.f - gv[j][k];
+        const float keep = gk[j][k];
         const float mr = lr[k] * Br[k] - li[k] * Bi[k];
         const float mi = lr[k] * Bi[k] + li[k] * Br[k];
         Br[k] = fmaf(keep, mr, gbr[j][k]);
@@ -319,13 +323,13 @@ struct WaveTile {
         float dr[K], di[K];
 #pragma unroll
         for (int k = 0; k < K; ++k) {
-          // m = lam*s_prev, disp = v*m, s = (1-v)*m + b
+          // m = lam*s_prev, disp = v*m = m - keep*m, s = keep*m + b
           const float mr = lr[k] * sr[k] - li[k] * si[k];
           const float mi = lr[k] * si[k] + li[k] * sr[k];
-          dr[k] = gv[j][k] * mr;
-          di[k] = gv[j][k] * mi;
-          sr[k] = (mr - dr[k]) + gbr[j][k];
-          si[k] = (mi - di[k]) + gbi[j][k];
+          dr[k] = fmaf(-gk[j][k], mr, mr);
+          di[k] = fmaf(-gk[j][k], mi, mi);
+          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
+          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
         }
         const int so = so0 + j * row_bytes;
         ReadStore<OutT, K>::run(w, vo, so, sr);
@@ -352,9 +356,9 @@ struct WaveTile {
         for (int k = 0; k < K; ++k) {
           const float mr = lr[k] * sr[k] - li[k] * si[k];
           const float mi = lr[k] * si[k] + li[k] * sr[k];
-          const float dr = gv[j][k] * mr, di = gv[j][k] * mi;
-          sr[k] = (mr - dr) + gbr[j][k];
-          si[k] = (mi - di) + gbi[j][k];
+          const float dr = fmaf(-gk[j][k], mr, mr), di = fmaf(-gk[j][k], mi, mi);
+          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
+          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
           acc = fmaf(sr[k], sr[k], acc);
           acc = fmaf(si[k], si[k], acc);
           acc = fmaf(dr, dr, acc);
@@ -383,9 +387,9 @@ struct WaveTile {
         for (int k = 0; k < K; ++k) {
           const float mr = lr[k] * sr[k] - li[k] * si[k];
           const float mi = lr[k] * si[k] + li[k] * sr[k];
-          const float dr = gv[j][k] * mr, di = gv[j][k] * mi;
-          sr[k] = (mr - dr) + gbr[j][k];
-          si[k] = (mi - di) + gbi[j][k];
+          const float dr = fmaf(-gk[j][k], mr, mr), di = fmaf(-gk[j][k], mi, mi);
+          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
+          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
           o[0][k] = (sr[k] * sc) * nw[0][k];
           o[1][k] = (si[k] * sc) * nw[1][k];
           o[2][k] = (dr * sc) * nw[2][k];
@@ -1527,14 +1531,14 @@ __global__ __launch_bounds__(256) void fl_decode_step_kernel(
   float dr[K], di[K];
 #pragma unroll
   for (int k = 0; k < K; ++k) {
-    float v, br, bi;
-    gates(zr[k], zi[k], zv[k], gm[k], v, br, bi);
+    float keep, br, bi;
+    gates(zr[k], zi[k], zv[k], kVacancyMax * gm[k], keep, br, bi);
     const float mr = lr[k] * sr[k] - li[k] * si[k];
     const float mi = lr[k] * si[k] + li[k] * sr[k];
-    dr[k] = v * mr;
-    di[k] = v * mi;
-    sr[k] = (mr - dr[k]) + br;
-    si[k] = (mi - di[k]) + bi;
+    dr[k] = fmaf(-keep, mr, mr);
+    di[k] = fmaf(-keep, mi, mi);
+    sr[k] = fmaf(keep, mr, br);
+    si[k] = fmaf(keep, mi, bi);
   }
   Store<K>::run(s, sr);
   Store<K>::run(s + C, si);
@@ -1555,14 +1559,14 @@ constexpr int kDecodeNormThreads = 256;
 
 __device__ __forceinline__ void decode_one(float zr, float zi, float zv, float lr, float li,
                                            float gm, float& sr, float& si, float& dr, float& di) {
-  float v, br, bi;
-  gates(zr, zi, zv, gm, v, br, bi);
+  float keep, br, bi;
+  gates(zr, zi, zv, kVacancyMax * gm, keep, br, bi);
   const float mr = lr * sr - li * si;
   const float mi = lr * si + li * sr;
-  dr = v * mr;
-  di = v * mi;
-  sr = (mr - dr) + br;
-  si = (mi - di) + bi;
+  dr = fmaf(-keep, mr, mr);
+  di = fmaf(-keep, mi, mi);
+  sr = fmaf(keep, mr, br);
+  si = fmaf(keep, mi, bi);
 }
 
 __device__ __forceinline__ void store_out(float* p, float v) { *p = v; }
