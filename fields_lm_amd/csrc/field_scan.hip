@@ -1367,12 +1367,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           const float v = gv[j][k], keep = 1.f - v;
-          const float ur = __builtin_amdgcn_exp2f(fabsf(zr[j][k]) * (-2.0f * kLog2e));
-          const float ui = __builtin_amdgcn_exp2f(fabsf(zi[j][k]) * (-2.0f * kLog2e));
-          const float er = 1.0f + ur, ei = 1.0f + ui;
-          const float rdi = __builtin_amdgcn_rcpf(er * ei);
-          const float injr = copysignf((1.0f - ur) * (ei * rdi), zr[j][k]);
-          const float inji = copysignf((1.0f - ui) * (er * rdi), zi[j][k]);
+          // tanh = 1 - 2 / (1 + e^{2z}), as in the forward gates
+          const float injr = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zr[j][k] * (2.0f * kLog2e))), 1.0f);
+          const float inji = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zi[j][k] * (2.0f * kLog2e))), 1.0f);
           const float Gr = uR[j][k] + car[k], Gi = uI[j][k] + cai[k];
           const float p_r = pr[j][k], p_i = pi[j][k];
           const float mr = lr[k] * p_r - li[k] * p_i;     // lam p
