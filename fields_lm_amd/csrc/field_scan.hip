@@ -921,8 +921,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     s_tk[1] = (uint32_t)(tk >> 32);
   }
   __syncthreads();
-  const uint32_t ticket = s_tk[0];
-  const uint32_t epoch = s_tk[1];
+  // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
+  const uint32_t ticket = (uint32_t)uniform((int)s_tk[0]);
+  const uint32_t epoch = (uint32_t)uniform((int)s_tk[1]);
   if (ticket >= n_tiles) {  // counter not re-armed by an interrupted launch: refuse, terminate
     if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
     return;
@@ -1140,7 +1141,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ read, const float* __restrict__ grad_read,
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ pgrad, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split) {
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split, uint32_t n_chains) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1159,13 +1160,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     s_tk[1] = (uint32_t)(tk >> 32);
   }
   __syncthreads();
-  const uint32_t ticket = s_tk[0];
-  const uint32_t epoch = s_tk[1];
+  // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
+  const uint32_t ticket = (uint32_t)uniform((int)s_tk[0]);
+  const uint32_t epoch = (uint32_t)uniform((int)s_tk[1]);
   if (ticket >= n_tiles) {
     if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
     return;
   }
-  const uint32_t n_chains = n_tiles / (uint32_t)n_chunks;
   const int ord = (int)(ticket / n_chains);
   const int chain = (int)(ticket - (uint32_t)ord * n_chains);
   const int chunk = n_chunks - 1 - ord;
@@ -1341,8 +1342,12 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     float zr[L][K], zi[L][K], pr[L][K], pi[L][K];
     {
       const bool first = t_begin == 0;
-      const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + (first ? 0 : t_begin - 1)) * 4 * C,
-                                      (uint32_t)((int64_t)(first ? rows : rows + 1) * 4 * C * 4));
+      // row and row count forced wave-uniform: a descriptor the compiler takes for divergent
+      // costs a readfirstlane loop around every load through it
+      const int prev_row = uniform(first ? t_begin : t_begin - 1);
+      const int prev_rows = uniform(first ? rows : rows + 1);
+      const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + prev_row) * 4 * C,
+                                      (uint32_t)((int64_t)prev_rows * 4 * C * 4));
 #pragma unroll
       for (int j = 0; j < L; ++j) {
         RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
@@ -2072,7 +2077,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma,
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad,
       reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
-      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split);
+      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split, (uint32_t)n_chains);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
   float* seg = reinterpret_cast<float*>(ws + lay.seg_off);

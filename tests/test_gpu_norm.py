@@ -45,9 +45,10 @@ def _to(dev, *ts):
     return [t.to(dev).contiguous() for t in ts]
 
 
-# C = 48, 6, 5: one partial channel tile; 512: 8 tiles; 1024: 16; 4096: 64 (the maximum)
+# C = 48, 6, 5: one partial channel tile; 512: 8 tiles; 1024: 16; 4096: 64 (the maximum);
+# (16, 1000, 512), (24, 700, 200): tickets in chain groups, sibling tiles inside one group
 SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
-          (4, 257, 512), (2, 1000, 1024), (1, 300, 4096)]
+          (4, 257, 512), (2, 1000, 1024), (1, 300, 4096), (16, 1000, 512), (24, 700, 200)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
