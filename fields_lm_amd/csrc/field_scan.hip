@@ -1130,7 +1130,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 //   dv  = Re(conj(D) lam p) - Re(conj(G) lam p) + gamma Re(conj(G) inj),  dzv = dv v (1 - v/0.9),
 //   dlam += (1 - v) G conj(p) + v D conj(p),   dgamma += v Re(conj(G) inj),
 // and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
-// then the waves in order) into per-tile partials that fl_param_grad_reduce_kernel adds up over
+// then the waves in order) into per-tile partials that fl_param_grad_{segment,final}_kernel add up over
 // the tiles of each channel in a fixed order (deterministic).
 // ------------------------------------------------------------------------------------------
 template <typename RawT, typename GradT, int K, int L, int W, int OCC>
@@ -1444,11 +1444,14 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 
 // Sum of the per-tile parameter-gradient partials over the batch rows and chunks of each
 // channel, in two deterministic stages: fl_param_grad_segment_kernel adds the partial rows of
-// one segment of (at least kReduceSegRows) rows for 64 channels (waves over interleaved rows, then the
-// waves in order), fl_param_grad_final_kernel adds the segments in order into grad_tr/ti/gamma
-// (overwritten). Many segments keep the whole chip busy when B * n_chunks is large.
+// one segment of (at least kReduceSegRows) rows for 64 channels (waves over interleaved rows, then
+// the waves in order), fl_param_grad_final_kernel adds the segments of 64 channels (waves over
+// interleaved segments, kFinalBatch loads in flight, then the waves in order) into
+// grad_tr/ti/gamma (overwritten). Many segments keep the whole chip busy when B * n_chunks is
+// large; every sum runs in a fixed order, so the gradients are bit-reproducible.
 constexpr int kReduceWaves = 4;
-constexpr int kReduceSegRows = 32;
+constexpr int kReduceSegRows = 16;
+constexpr int kFinalBatch = 8;
 
 __global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_segment_kernel(
     const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT, int seg_rows,
@@ -1487,21 +1490,40 @@ __global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_segment_kerne
   }
 }
 
-__global__ __launch_bounds__(256) void fl_param_grad_final_kernel(
+__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_final_kernel(
     const float* __restrict__ seg, int n_seg, int C, float* __restrict__ grad_tr,
     float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= C) return;
-  float t0 = 0.f, t1 = 0.f, t2 = 0.f;
-  for (int i = 0; i < n_seg; ++i) {
-    const float* p = seg + (size_t)i * 3 * C + c;
-    t0 += p[0];
-    t1 += p[C];
-    t2 += p[2 * C];
+  __shared__ float s_acc[kReduceWaves][3][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int c = blockIdx.x * 64 + lane;
+  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+  if (c < C) {
+    for (int i0 = wave; i0 < n_seg; i0 += kReduceWaves * kFinalBatch) {
+      float v[kFinalBatch][3];
+#pragma unroll
+      for (int q = 0; q < kFinalBatch; ++q) {
+        const int i = i0 + q * kReduceWaves;
+        const float* p = seg + (size_t)i * 3 * C + c;
+        v[q][0] = i < n_seg ? p[0] : 0.f;
+        v[q][1] = i < n_seg ? p[C] : 0.f;
+        v[q][2] = i < n_seg ? p[2 * C] : 0.f;
+      }
+#pragma unroll
+      for (int q = 0; q < kFinalBatch; ++q) { a0 += v[q][0]; a1 += v[q][1]; a2 += v[q][2]; }
+    }
   }
-  grad_tr[c] = t0;
-  grad_ti[c] = t1;
-  grad_gamma[c] = t2;
+  s_acc[wave][0][lane] = a0;
+  s_acc[wave][1][lane] = a1;
+  s_acc[wave][2][lane] = a2;
+  __syncthreads();
+  if (wave == 0 && c < C) {
+    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+    for (int w = 0; w < kReduceWaves; ++w) { t0 += s_acc[w][0][lane]; t1 += s_acc[w][1][lane]; t2 += s_acc[w][2][lane]; }
+    grad_tr[c] = t0;
+    grad_ti[c] = t1;
+    grad_gamma[c] = t2;
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2086,8 +2108,8 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
                                                                  g.n_ctiles, CT, lay.seg_rows, seg);
   e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
-  fl_param_grad_final_kernel<<<(unsigned)cdiv(C, 256), 256, 0, stream>>>(seg, lay.n_seg, (int)C, grad_tr,
-                                                                        grad_ti, grad_gamma);
+  fl_param_grad_final_kernel<<<(unsigned)cdiv(C, 64), kReduceWaves * 64, 0, stream>>>(
+      seg, lay.n_seg, (int)C, grad_tr, grad_ti, grad_gamma);
   return hip_status(hipGetLastError());
 }
 

@@ -207,3 +207,33 @@ def test_field_block_training_gradients(dev):
     (yd * w.double()).sum().backward()
     for k, p in cpu.named_parameters():
         assert oracle.rel_err(got[k], p.grad) <= 2e-4, k
+
+
+def test_backward_workspace_reuse_across_shapes(dev):
+    """One backward workspace (the per-stream cache), calls alternating shape: the parameter
+    gradients of every call equal those of the shape's first call bit for bit (the reduction's
+    per-column counts start at 0 whatever an earlier shape left in the workspace)."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    print("[case] backward workspace reuse", flush=True)
+    cases = []
+    for i, (B, T, C) in enumerate([(2, 900, 256), (3, 300, 512), (1, 4099, 64), (16, 1000, 512)]):
+        g = torch.Generator().manual_seed(60 + i)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dev)
+        tr, ti, gamma = (t.to(dev) for t in _params(C, 60 + i))
+        read = field_scan(raw, tr, ti, gamma)
+        gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+        cases.append((raw, tr, ti, gamma, read, gread))
+    first = [None] * len(cases)
+    for rep in range(3):
+        for i in ([0, 1, 2, 3] if rep % 2 == 0 else [3, 1, 0, 2]):
+            raw, tr, ti, gamma, read, gread = cases[i]
+            got = [x.clone() for x in field_scan_backward(raw, tr, ti, gamma, read, gread)[1:]]
+            if first[i] is None:
+                first[i] = got
+                _, e_tr, e_ti, e_gm, _ = _oracle_grads(raw.cpu(), tr.cpu(), ti.cpu(), gamma.cpu(), gread.cpu())
+                for a, e in zip(got, (e_tr, e_ti, e_gm)):
+                    assert oracle.rel_err(a.cpu(), e) <= TOL, i
+            else:
+                for a, b in zip(got, first[i]):
+                    torch.testing.assert_close(a, b, rtol=0, atol=0)
