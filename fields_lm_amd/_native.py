@@ -130,5 +130,5 @@ def scan_workspace(device: torch.device, nbytes: int, kind: str = "forward") -> 
 def workspace_error(ws: torch.Tensor) -> int:
     """Error word of a scan workspace header (0 = every look-back wait completed).
 
-    Header: bytes 0..3 tiles done, 128..131 error bits, 256.. ticket counters (one per 128 B)."""
+    Header: bytes 0..3 tiles done, 128..131 error bits, 256..263 epoch and ticket counter."""
     return int(ws[128:132].view(torch.int32).item())

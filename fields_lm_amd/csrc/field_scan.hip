@@ -688,16 +688,17 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // Waits sleep between polls and give up after kSpinLimit polls (error flag set), so every
 // wave terminates.
 // ------------------------------------------------------------------------------------------
-constexpr int kTicketCounters = 8;  // at most S counters
-// Every word sits in its own 128-byte line: counters are hammered by the blocks' first atomic,
-// `done` by their last one.
+// Every word sits in its own 128-byte line: the ticket counter is hammered by the blocks' first
+// atomic (long chains), `done` by their last one.
 struct LookbackHeader {
   unsigned int done;   // tiles finished in this launch
   unsigned int pad0[31];
   unsigned int error;  // bit 0: a wait hit kSpinLimit; bit 1: ticket out of range
   unsigned int pad1[31];
-  // counter x: bits 63..32 launch epoch, bits 31..0 tickets taken in this launch
-  unsigned long long ticket[kTicketCounters][16];
+  // bits 63..32 launch epoch, bits 31..0 tickets taken in this launch (block-order launches
+  // only read the epoch)
+  unsigned long long ticket;
+  unsigned long long pad2[15];
 };
 
 constexpr uint32_t kTagAgg = 1u;
@@ -901,7 +902,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split, bool in_order,
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, bool in_order,
     const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
@@ -917,16 +918,15 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   uint32_t ticket;
   uint64_t epoch_word = 0;
   if (in_order) {
-    // block i takes tile i; the epoch (counter 0's high word) is loaded now and stored to LDS
+    // block i takes tile i; the epoch (the counter's high word) is loaded now and stored to LDS
     // once the raw loads issued after it have landed
     ticket = blockIdx.x;
     if (wave == 0)
-      epoch_word = __hip_atomic_load(&hdr->ticket[0][0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      epoch_word = __hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     if (threadIdx.x == 0) {
-      const uint32_t x = blockIdx.x % n_split;
-      const unsigned long long tk = atomicAdd(&hdr->ticket[x][0], 1ull);
-      s_tk[0] = (uint32_t)tk * n_split + x;
+      const unsigned long long tk = atomicAdd(&hdr->ticket, 1ull);
+      s_tk[0] = (uint32_t)tk;
       s_tk[1] = (uint32_t)(tk >> 32);
     }
     __syncthreads();
@@ -1118,8 +1118,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const unsigned int d = atomicAdd(&hdr->done, 1u);
     if (d == n_tiles - 1) {
       const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
-      for (int x = 0; x < kTicketCounters; ++x)
-        __hip_atomic_store(&hdr->ticket[x][0], armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -1152,7 +1151,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ read, const float* __restrict__ grad_read,
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ pgrad, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_split, uint32_t n_chains) {
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_chains,
+    bool in_order) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1164,19 +1164,25 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
-  if (threadIdx.x == 0) {
-    const uint32_t x = blockIdx.x % n_split;
-    const unsigned long long tk = atomicAdd(&hdr->ticket[x][0], 1ull);
-    s_tk[0] = (uint32_t)tk * n_split + x;
-    s_tk[1] = (uint32_t)(tk >> 32);
-  }
-  __syncthreads();
-  // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
-  const uint32_t ticket = (uint32_t)uniform((int)s_tk[0]);
-  const uint32_t epoch = (uint32_t)uniform((int)s_tk[1]);
-  if (ticket >= n_tiles) {
-    if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
-    return;
+  uint32_t ticket;
+  uint64_t epoch_word = 0;
+  if (in_order) {  // block i takes tile i, as in the forward kernel
+    ticket = blockIdx.x;
+    if (wave == 0)
+      epoch_word = __hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    if (threadIdx.x == 0) {
+      const unsigned long long tk = atomicAdd(&hdr->ticket, 1ull);
+      s_tk[0] = (uint32_t)tk;
+      s_tk[1] = (uint32_t)(tk >> 32);
+    }
+    __syncthreads();
+    // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
+    ticket = (uint32_t)uniform((int)s_tk[0]);
+    if (ticket >= n_tiles) {
+      if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
+      return;
+    }
   }
   const int ord = (int)(ticket / n_chains);
   const int chain = (int)(ticket - (uint32_t)ord * n_chains);
@@ -1185,8 +1191,6 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   const int ctile = chain - b * n_ctiles;
   const int c0 = ctile * CT + lane * K;
   const bool ok = c0 < C;
-  const uint32_t tag_agg = ((epoch & 0x3fffffffu) << 2) | kTagAgg;
-  const uint32_t tag_incl = ((epoch & 0x3fffffffu) << 2) | kTagIncl;
   const int t_begin = chunk * TC;
   const bool last_ord = ord == n_chunks - 1;
 
@@ -1225,6 +1229,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     for (int k = 0; k < K; ++k)
       gv[j][k] = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv[k] * -kLog2e));
   }
+  if (in_order && threadIdx.x == 0) s_tk[1] = (uint32_t)(epoch_word >> 32);
   {
     // wave map from its right edge to its left edge over its valid rows (reverse order)
     float P[K], Qr[K], Qi[K];
@@ -1263,6 +1268,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     if (nu == L) { pr = cLr[k]; pi = cLi[k]; } else { cpow(clr[k], cli[k], nu, pr, pi); }
   };
   __syncthreads();
+  const uint32_t epoch = (uint32_t)uniform((int)s_tk[1]);
+  const uint32_t tag_agg = ((epoch & 0x3fffffffu) << 2) | kTagAgg;
+  const uint32_t tag_incl = ((epoch & 0x3fffffffu) << 2) | kTagIncl;
 
   const uint32_t tile_id = (uint32_t)chain * (uint32_t)n_chunks + (uint32_t)ord;
   uint32_t* st_chain = status + (size_t)chain * n_chunks;
@@ -1446,8 +1454,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const unsigned int d = atomicAdd(&hdr->done, 1u);
     if (d == n_tiles - 1) {
       const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
-      for (int x = 0; x < kTicketCounters; ++x)
-        __hip_atomic_store(&hdr->ticket[x][0], armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
@@ -1987,12 +1994,11 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // start, which the look-back needs to keep up (B=1, T=65,536: 155 us; 203 us in block order,
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
-  const uint32_t n_split = 1;
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
-      g.n_tiles, n_split, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)),
+      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)),
       reinterpret_cast<uint64_t*>(ws + lay.sib_off));
   return hip_status(hipGetLastError());
 }
@@ -2105,14 +2111,14 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const LookbackGeom& g = lay.g;
   char* ws = static_cast<char*>(workspace);
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
-  uint32_t n_split = g.n_chunks <= 64 ? kTicketCounters : 1;
-  while (n_chains % n_split) n_split /= 2;
+  // ticket order as in the forward launch: block order for short chains, one counter otherwise
+  const bool in_order = g.n_chunks <= 64;
   float* pgrad = reinterpret_cast<float*>(ws + lay.pgrad_off);
   fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ><<<g.n_tiles, tl.w * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma,
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad,
       reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
-      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, n_split, (uint32_t)n_chains);
+      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, (uint32_t)n_chains, in_order);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
   float* seg = reinterpret_cast<float*>(ws + lay.seg_off);
