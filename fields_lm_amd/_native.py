@@ -46,7 +46,7 @@ SIGNATURES = {
     "fl_scan_backward": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp,
                                 _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp, _vp, _sz, _vp]),
     "fl_scan_backward_workspace_bytes": (_sz, [_i64, _i64, _i64]),
-    "fl_gate_residual_norm": (_int, [_vp, _int, _vp, _vp, _int, _i64, _i64, _vp, ctypes.c_float,
+    "fl_gate_residual_norm": (_int, [_vp, _int, _vp, _vp, _int, _i64, _i64, _i64, _vp, ctypes.c_float,
                                      _vp, _vp, _vp]),
     "fl_swiglu": (_int, [_vp, _int, _i64, _i64, _vp, _vp]),
     "fl_boundary_scan": (_int, [_vp, _vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp]),

@@ -1778,13 +1778,14 @@ constexpr int kTailThreads = 256;
 
 template <typename XT, typename GT, int NPER>
 __global__ __launch_bounds__(kTailThreads) void fl_gate_residual_norm_kernel(
-    const XT* __restrict__ x, const GT* __restrict__ out, const GT* __restrict__ gpre, int dim,
-    const float* __restrict__ w, float eps, float inv_dim, XT* __restrict__ x_new,
-    XT* __restrict__ normed) {
+    const XT* __restrict__ x, const GT* __restrict__ out, const GT* __restrict__ gpre,
+    int64_t gstride, int dim, const float* __restrict__ w, float eps, float inv_dim,
+    XT* __restrict__ x_new, XT* __restrict__ normed) {
   __shared__ float s_red[kTailThreads / 64];
   const int64_t base = (int64_t)blockIdx.x * dim;
+  const GT* grow = gpre + (int64_t)blockIdx.x * gstride;
   auto residual = [&](int c) {
-    const float gate = round_as<GT>(1.0f / (1.0f + expf(-load_as<GT>(gpre + base + c))));
+    const float gate = round_as<GT>(1.0f / (1.0f + expf(-load_as<GT>(grow + c))));
     const float prod = round_as<GT>(load_as<GT>(out + base + c) * gate);
     return round_as<XT>(load_as<XT>(x + base + c) + prod);
   };
@@ -2353,13 +2354,15 @@ int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64
 }
 
 int fl_gate_residual_norm(const void* x, int x_dtype, const void* out, const void* gate_pre,
-                          int g_dtype, int64_t rows, int64_t dim, const float* norm_weight,
-                          float eps, void* x_new, void* normed, void* stream) {
+                          int g_dtype, int64_t rows, int64_t dim, int64_t gate_stride,
+                          const float* norm_weight, float eps, void* x_new, void* normed,
+                          void* stream) {
   if ((x_dtype != FL_DTYPE_F32 && x_dtype != FL_DTYPE_BF16) ||
       (g_dtype != FL_DTYPE_F32 && g_dtype != FL_DTYPE_BF16))
     return FL_ERR_DTYPE;
   if (rows <= 0 || dim <= 0 || rows > ((int64_t)1 << 31) - 1 || dim > ((int64_t)1 << 24))
     return FL_ERR_INVALID_ARGUMENT;
+  if (gate_stride < dim || gate_stride > ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!x || !out || !gate_pre || !norm_weight || !x_new || !normed || !(eps >= 0.f))
     return FL_ERR_INVALID_ARGUMENT;
   const size_t xs = x_dtype == FL_DTYPE_BF16 ? 2 : 4, gs = g_dtype == FL_DTYPE_BF16 ? 2 : 4;
@@ -2371,7 +2374,8 @@ int fl_gate_residual_norm(const void* x, int x_dtype, const void* out, const voi
 #define FL_GRN1(X, G, N)                                                                        \
   fl_gate_residual_norm_kernel<X, G, N><<<(unsigned)rows, kTailThreads, 0, s>>>(                \
       static_cast<const X*>(x), static_cast<const G*>(out), static_cast<const G*>(gate_pre),    \
-      (int)dim, norm_weight, eps, inv, static_cast<X*>(x_new), static_cast<X*>(normed));        \
+      gate_stride, (int)dim, norm_weight, eps, inv, static_cast<X*>(x_new),                     \
+      static_cast<X*>(normed));                                                                 \
   return hip_status(hipGetLastError());
 #define FL_GRN(X, G)                                                                            \
   if (dim <= kTailThreads) { FL_GRN1(X, G, 1) }                                                 \

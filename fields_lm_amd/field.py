@@ -350,12 +350,33 @@ def boundary_scan(a: torch.Tensor, drive: torch.Tensor, state_in: Optional[torch
     return (out, sout) if return_state else out
 
 
+def _row_stride(t: torch.Tensor) -> Optional[int]:
+    """Element distance between consecutive rows of ``t`` viewed as [rows, t.shape[-1]] when its
+    last dimension is unit-stride and every leading dimension steps whole rows (a column slice of
+    a contiguous tensor); None otherwise."""
+    if t.ndim == 0 or t.stride(-1) != 1:
+        return None
+    if t.ndim == 1:
+        return t.shape[-1]
+    rs = t.stride(-2)
+    if rs < t.shape[-1]:
+        return None
+    step = rs
+    for i in range(t.ndim - 2, 0, -1):
+        step *= t.shape[i]
+        if t.shape[i - 1] > 1 and t.stride(i - 1) != step:
+            return None
+    return rs
+
+
 def gate_residual_norm(x: torch.Tensor, out: torch.Tensor, gate_pre: torch.Tensor,
                        weight: torch.Tensor, eps: float = 1e-6) -> Tuple[torch.Tensor, torch.Tensor]:
     """``x + out * sigmoid(gate_pre)`` and its RMSNorm (``fl_gate_residual_norm``): the mixer's
     gated residual (canon:1193-1195) and the block's ``ff_norm`` (canon:1219-1221) in one launch,
     rounded as the stock ops round. x: residual stream (fp32 / bf16); out, gate_pre: the out_proj /
-    gate_proj outputs; all [..., dim] on one device. Returns (x_new, normed) in x's dtype."""
+    gate_proj outputs; all [..., dim] on one device. ``gate_pre`` may be a column slice of a wider
+    GEMM output (rows a fixed stride apart); the others are made contiguous. Returns (x_new,
+    normed) in x's dtype."""
     lib = nat.load()
     if not x.is_cuda:
         raise RuntimeError("gate_residual_norm requires a ROCm (cuda) device")
@@ -364,15 +385,20 @@ def gate_residual_norm(x: torch.Tensor, out: torch.Tensor, gate_pre: torch.Tenso
     dim = x.shape[-1]
     if weight.numel() != dim:
         raise ValueError("weight must have dim entries")
-    x, out, gate_pre = x.contiguous(), out.contiguous(), gate_pre.contiguous()
+    x, out = x.contiguous(), out.contiguous()
+    gate_stride = _row_stride(gate_pre)
+    if gate_stride is None:
+        gate_pre = gate_pre.contiguous()
+        gate_stride = dim
     w = weight.detach().to(device=x.device, dtype=torch.float32).contiguous()
     x_new, normed = torch.empty_like(x), torch.empty_like(x)
     rows = x.numel() // dim if dim else 0
     if rows == 0:
         return x_new, normed
     code = lib.fl_gate_residual_norm(nat.ptr(x), nat.dtype_code(x.dtype), nat.ptr(out), nat.ptr(gate_pre),
-                                     nat.dtype_code(out.dtype), rows, dim, nat.ptr(w), ctypes.c_float(float(eps)),
-                                     nat.ptr(x_new), nat.ptr(normed), nat.stream_handle(x.device))
+                                     nat.dtype_code(out.dtype), rows, dim, gate_stride, nat.ptr(w),
+                                     ctypes.c_float(float(eps)), nat.ptr(x_new), nat.ptr(normed),
+                                     nat.stream_handle(x.device))
     nat.check(code, "fl_gate_residual_norm")
     return x_new, normed
 
@@ -470,6 +496,10 @@ class IndependentVacancyField(nn.Module):
         # fl_decode_norm_step) and the fp32 read never reaches memory; False: the scan writes
         # read and read_norm runs as a separate module call, as in the reference.
         self.fuse_read_norm = True
+        # True: without gradients, write_proj and gate_proj run as one GEMM (in_proj). Not a
+        # parameter or buffer: state_dict is unchanged.
+        self.fuse_in_proj = True
+        self._packed = None  # (key, weight, bias) of the stacked projections
 
     def transition(self) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """(tr, ti, gamma) fp32 [C] (canon:1169-1173), computed in the parameters' dtype."""
@@ -480,13 +510,39 @@ class IndependentVacancyField(nn.Module):
         gamma = torch.sqrt((1.0 - radius.square()).clamp_min(1e-4))
         return tr.contiguous(), ti.contiguous(), gamma.contiguous()
 
-    def _raw(self, x: torch.Tensor) -> torch.Tensor:
+    def _raw(self, x: torch.Tensor, raw: Optional[torch.Tensor] = None) -> torch.Tensor:
         # bf16 (autocast) and fp32 raw go to the kernel as they are; the kernel's upcast of
         # bf16 is exact, so this equals the reference's `.contiguous().float()` copy.
-        raw = self.write_proj(x)
+        if raw is None:
+            raw = self.write_proj(x)
         if raw.dtype not in (torch.float32, torch.bfloat16):
             raw = raw.float()
         return raw
+
+    def _no_grad(self, x: torch.Tensor) -> bool:
+        return not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())))
+
+    def in_proj(self, x: torch.Tensor) -> Tuple[torch.Tensor, torch.Tensor]:
+        """(raw, gate_pre) = (write_proj(x), gate_proj(x)). Without gradients the two run as one
+        GEMM over their weights stacked ([write_proj; gate_proj], a packed copy rebuilt whenever a
+        weight or bias changes): raw and gate_pre are column slices of its output, which the scan,
+        the decode step and the fused tail read in place (row stride dim + C + dim)."""
+        if not (self.fuse_in_proj and self._no_grad(x)):
+            return self.write_proj(x), self.gate_proj(x)
+        w, b = self._packed_in_proj()
+        y = F.linear(x, w, b)
+        n = self.write_proj.out_features
+        return y[..., :n], y[..., n:]
+
+    def _packed_in_proj(self) -> Tuple[torch.Tensor, torch.Tensor]:
+        srcs = (self.write_proj.weight, self.write_proj.bias, self.gate_proj.weight, self.gate_proj.bias)
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs)
+        if self._packed is None or self._packed[0] != key:
+            with torch.no_grad():
+                w = torch.cat([srcs[0], srcs[2]], 0)
+                b = torch.cat([srcs[1], srcs[3]], 0)
+            self._packed = (key, w, b)
+        return self._packed[1], self._packed[2]
 
     def _readout(self, x: torch.Tensor, read: torch.Tensor) -> torch.Tensor:
         return self._project(x, self.read_norm(read))
@@ -511,10 +567,11 @@ class IndependentVacancyField(nn.Module):
             return torch.bfloat16 if raw.dtype == torch.bfloat16 else torch.float32
         return self.read_dtype
 
-    def normed_read(self, x: torch.Tensor) -> torch.Tensor:
-        """read_norm(read) of the scan of x: what out_proj consumes."""
+    def normed_read(self, x: torch.Tensor, raw: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """read_norm(read) of the scan of x: what out_proj consumes (``raw`` = write_proj(x) when
+        already computed)."""
         tr, ti, gamma = self.transition()
-        raw = self._raw(x)
+        raw = self._raw(x, raw)
         if self._fused(x):
             return _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
                                                 self.read_norm.eps, self._read_dtype(raw))
@@ -525,11 +582,11 @@ class IndependentVacancyField(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self._project(x, self.normed_read(x))
 
-    def normed_prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
-                       ) -> Tuple[torch.Tensor, torch.Tensor]:
+    def normed_prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None,
+                       raw: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
         """read_norm(read) over [B,T,dim] and the recurrent state s[T-1] (fp32 [B,2C])."""
         tr, ti, gamma = self.transition()
-        raw = self._raw(x)
+        raw = self._raw(x, raw)
         if self._fused(x):
             return field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight, self.read_norm.eps,
                                    state_in=state, return_state=True, out_dtype=self._read_dtype(raw))
@@ -561,11 +618,12 @@ class IndependentVacancyField(nn.Module):
         return self._project(x_t, self.normed_step(x_t, state, params))
 
     def normed_step(self, x_t: torch.Tensor, state: torch.Tensor,
-                    params: Optional[Tuple[torch.Tensor, ...]] = None) -> torch.Tensor:
+                    params: Optional[Tuple[torch.Tensor, ...]] = None,
+                    raw_t: Optional[torch.Tensor] = None) -> torch.Tensor:
         """read_norm(read_t) of one decode token; ``state`` advances in place."""
         params = params if params is not None else self.decode_params()
         tr, ti, gamma = params[:3]
-        raw_t = self._raw(x_t)
+        raw_t = self._raw(x_t, raw_t)
         if self._fused(x_t):
             w = params[3] if len(params) > 3 else self.read_norm.weight.detach().float().contiguous()
             return field_decode_norm_step(raw_t, tr, ti, gamma, state, w, self.read_norm.eps,
@@ -598,29 +656,32 @@ class FieldBlock(nn.Module):
             return False
         return not (torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters())))
 
-    def _tail(self, x: torch.Tensor, normed: torch.Tensor) -> torch.Tensor:
+    def _tail(self, x: torch.Tensor, normed: torch.Tensor, gate_pre: torch.Tensor) -> torch.Tensor:
         m = self.mixer
-        x1, h = gate_residual_norm(x, m.out_proj(normed), m.gate_proj(x), self.ff_norm.weight, self.ff_norm.eps)
+        x1, h = gate_residual_norm(x, m.out_proj(normed), gate_pre, self.ff_norm.weight, self.ff_norm.eps)
         first, second = (self.ff.w12, self.ff.w3) if hasattr(self.ff, "w12") else (self.ff.gate_up, self.ff.down)
         return x1 + second(swiglu(first(h)))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self._fused_tail(x):
-            return self._tail(x, self.mixer.normed_read(x))
+            raw, gate_pre = self.mixer.in_proj(x)
+            return self._tail(x, self.mixer.normed_read(x, raw), gate_pre)
         x = self.mixer(x)
         return x + self.ff(self.ff_norm(x))
 
     def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
                 ) -> Tuple[torch.Tensor, torch.Tensor]:
         if self._fused_tail(x):
-            normed, state = self.mixer.normed_prefill(x, state)
-            return self._tail(x, normed), state
+            raw, gate_pre = self.mixer.in_proj(x)
+            normed, state = self.mixer.normed_prefill(x, state, raw)
+            return self._tail(x, normed, gate_pre), state
         x, state = self.mixer.prefill(x, state)
         return x + self.ff(self.ff_norm(x)), state
 
     def step(self, x_t: torch.Tensor, state: torch.Tensor, params=None) -> torch.Tensor:
         if self._fused_tail(x_t):
-            return self._tail(x_t, self.mixer.normed_step(x_t, state, params))
+            raw_t, gate_pre = self.mixer.in_proj(x_t)
+            return self._tail(x_t, self.mixer.normed_step(x_t, state, params, raw_t), gate_pre)
         x_t = self.mixer.step(x_t, state, params)
         return x_t + self.ff(self.ff_norm(x_t))
 

@@ -185,12 +185,15 @@ int fl_boundary_scan(const float* a, const float* drive, int64_t B, int64_t T, i
  *                                                    field_only_v4_chunked_triton_wiki100.py:1193-1195)
  *   normed = RMSNorm(x_new) * norm_weight           (FieldBlock.ff_norm, same file 1219-1221, 300-309)
  * out / gate_pre are the out_proj / gate_proj GEMM outputs (g_dtype), x / x_new / normed the
- * residual stream (x_dtype); all [rows, dim] contiguous. Every intermediate is rounded where the
- * stock ops round it (bf16 ops compute in fp32 and round their result).
+ * residual stream (x_dtype); all [rows, dim] contiguous except gate_pre, whose rows lie
+ * gate_stride >= dim elements apart (a column slice of a GEMM output that also holds other
+ * columns, e.g. write_proj and gate_proj computed in one GEMM). Every intermediate is rounded where
+ * the stock ops round it (bf16 ops compute in fp32 and round their result).
  */
 int fl_gate_residual_norm(const void* x, int x_dtype, const void* out, const void* gate_pre,
-                          int g_dtype, int64_t rows, int64_t dim, const float* norm_weight,
-                          float eps, void* x_new, void* normed, void* stream);
+                          int g_dtype, int64_t rows, int64_t dim, int64_t gate_stride,
+                          const float* norm_weight, float eps, void* x_new, void* normed,
+                          void* stream);
 
 /*
  * SwiGLU activation of the Field block FFN (PackedSwiGLU.forward, same file 312-325):

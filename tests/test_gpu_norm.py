@@ -415,3 +415,58 @@ def test_field_block_fused_tail_equals_stock_ops(dev):
     assert oracle.rel_err(torch.stack(steps, 1).cpu(), ref32[:, 50:].cpu()) <= 1e-4
     assert oracle.rel_err(got_gu.cpu(), ref_gu.cpu()) <= 1e-5
     assert oracle.rel_err(got16.float().cpu(), ref16.float().cpu()) <= 2e-2
+
+
+def test_gate_residual_norm_strided_gate(dev):
+    """gate_pre as a column slice of a wider GEMM output (rows a fixed stride apart) gives the
+    same bits as the contiguous copy; a slice whose rows are not evenly spaced is copied first."""
+    from fields_lm_amd import gate_residual_norm
+
+    print("[case] gate_residual_norm strided gate", flush=True)
+    g = torch.Generator(device=dev).manual_seed(41)
+    for dt in (torch.bfloat16, torch.float32):
+        x = torch.randn(3, 17, 1024, device=dev, generator=g).to(dt)
+        out = torch.randn(3, 17, 1024, device=dev, generator=g).to(dt)
+        wide = torch.randn(3, 17, 2560, device=dev, generator=g).to(dt)
+        w = torch.rand(1024, device=dev, generator=g) + 0.5
+        for gp in (wide[..., 1536:], wide[:, 2:9, 1536:]):
+            a = gate_residual_norm(x[:, :gp.shape[1]], out[:, :gp.shape[1]], gp, w)
+            b = gate_residual_norm(x[:, :gp.shape[1]], out[:, :gp.shape[1]], gp.contiguous(), w)
+            for u, v in zip(a, b):
+                torch.testing.assert_close(u, v, rtol=0, atol=0)
+
+
+def test_field_block_packed_in_proj(dev):
+    """Without gradients write_proj and gate_proj run as one GEMM over the stacked weights: the
+    block's forward, prefill and decode steps agree with the separate GEMMs, and the packed copy
+    follows an in-place weight update."""
+    from fields_lm_amd import FieldBlock
+
+    print("[case] FieldBlock packed in_proj", flush=True)
+    torch.manual_seed(43)
+    block = FieldBlock(256, "triton", 32, 32, 64, 512).to(dev)
+    x = torch.randn(2, 70, 256, device=dev)
+    with torch.no_grad():
+        block.mixer.fuse_in_proj = False
+        ref = block(x)
+        _, s_ref = block.prefill(x[:, :50])
+        steps_ref = [block.step(x[:, t], s_ref) for t in range(50, 70)]
+        block.mixer.fuse_in_proj = True
+        got = block(x)
+        _, s = block.prefill(x[:, :50])
+        steps = [block.step(x[:, t], s) for t in range(50, 70)]
+        assert oracle.rel_err(got.cpu(), ref.cpu()) <= 1e-5
+        assert oracle.rel_err(torch.stack(steps, 1).cpu(), torch.stack(steps_ref, 1).cpu()) <= 1e-5
+        assert oracle.rel_err(s.cpu(), s_ref.cpu()) <= 1e-5
+        block.mixer.gate_proj.weight.mul_(1.5)
+        block.mixer.write_proj.bias.add_(0.1)
+        got2 = block(x)
+        block.mixer.fuse_in_proj = False
+        ref2 = block(x)
+        assert oracle.rel_err(got2.cpu(), ref2.cpu()) <= 1e-5
+        assert oracle.rel_err(got2.cpu(), got.cpu()) > 1e-3
+        with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+            ref16 = block(x)
+            block.mixer.fuse_in_proj = True
+            got16 = block(x)
+        assert oracle.rel_err(got16.float().cpu(), ref16.float().cpu()) <= 2e-2
