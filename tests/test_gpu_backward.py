@@ -50,7 +50,8 @@ def _oracle_grads(raw, tr, ti, gamma, grad_read, state_in=None, grad_state_out=N
     return r.grad, p[0].grad, p[1].grad, p[2].grad, (None if s0 is None else s0.grad)
 
 
-# (16, 1000, 512), (24, 700, 200): tickets in chain groups (short chains, many tiles)
+# (16, 1000, 512), (24, 700, 200): more tiles than one round of resident blocks; (1, 4099, 64):
+# more than 64 chunks per chain (tickets from the counter)
 SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
           (4, 257, 512), (2, 1000, 1024), (1, 4099, 64), (16, 1000, 512), (24, 700, 200)]
 

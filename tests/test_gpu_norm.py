@@ -46,9 +46,11 @@ def _to(dev, *ts):
 
 
 # C = 48, 6, 5: one partial channel tile; 512: 8 tiles; 1024: 16; 4096: 64 (the maximum);
-# (16, 1000, 512), (24, 700, 200): tickets in chain groups, sibling tiles inside one group
+# (16, 1000, 512), (24, 700, 200): more tiles than one round of resident blocks; (2, 9000, 200):
+# more than 64 chunks per chain, tickets from the counter instead of in block order
 SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
-          (4, 257, 512), (2, 1000, 1024), (1, 300, 4096), (16, 1000, 512), (24, 700, 200)]
+          (4, 257, 512), (2, 1000, 1024), (1, 300, 4096), (16, 1000, 512), (24, 700, 200),
+          (2, 9000, 200)]
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])

@@ -41,10 +41,10 @@ def _to(dev, *ts):
     return [t.to(dev).contiguous() for t in ts]
 
 
-# (16, 1000, 512), (24, 700, 200): more tiles than one round of resident blocks with short
-# chains, so tickets run in chain groups (a group of 64 / 48 chains)
+# (16, 1000, 512), (24, 700, 200): more tiles than one round of resident blocks; (2, 9000, 64):
+# more than 64 chunks per chain, tickets from the counter instead of in block order
 SHAPES = [(2, 37, 32), (1, 1, 32), (3, 64, 48), (2, 100, 6), (2, 65, 5), (1, 130, 512),
-          (4, 257, 512), (2, 1000, 1024), (16, 1000, 512), (24, 700, 200)]
+          (4, 257, 512), (2, 1000, 1024), (16, 1000, 512), (24, 700, 200), (2, 9000, 64)]
 
 
 ALGOS = {"lookback": 2, "chunked3": 1}
