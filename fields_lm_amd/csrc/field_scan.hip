@@ -661,12 +661,13 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // Single-pass path (FL_ALGO_LOOKBACK): one launch, raw read once, read written once.
 //
 // Tiles = (chain = (b, channel tile), chunk of W*L steps); ticket -> tile is chunk-major, so the
-// predecessors of ticket t in its chain are t - n_chains, t - 2*n_chains, ... Each block takes
-// its ticket from one of S counters (S divides n_chains, counter = blockIdx mod S, ticket =
-// count*S + counter): a ticket's predecessors share its residue mod S, so they were taken
-// earlier from the same counter, by blocks that are already resident — a block only ever waits
-// on running blocks (no deadlock, whatever the dispatch order), and the S counters (one cache
-// line each) spread the start-of-launch atomics that a single counter would serialise. A tile
+// predecessors of ticket t in its chain are t - n_chains, t - 2*n_chains, ... and a tile only
+// waits on lower tickets. Tickets come either in block order (block i takes ticket i; the host's
+// choice for short chains) or from one atomic counter, in the order blocks start. From the
+// counter, a ticket's predecessors were taken earlier by blocks that are already running, whatever
+// the dispatch order. In block order, progress rests on the dispatcher issuing each XCD's share of
+// the grid in block order: every block resident ahead of the lowest unfinished tile on its XCD has
+// a lower index, so that tile is always resident. A tile
 //   1. loads its raw tile into registers and forms the gates;
 //   2. composes its summary (P, B) and publishes it (status AGG);
 //   3. looks back over its chain: the summaries of earlier tiles are composed until a tile
@@ -677,8 +678,9 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // With the RMSNorm epilogue (NORM), step 4 first runs the tile's recurrence once more without
 // storing, to form each row's partial sum of squares over the tile's channels; publishes the
 // partials (one word per row and channel tile); waits for the partials of the other channel
-// tiles of the same (batch row, chunk) — the n_ctiles consecutive tickets of its group, all
-// taken by blocks that are running or about to run, none of them waiting on this block — and
+// tiles of the same (batch row, chunk) — the n_ctiles consecutive tickets of its group, the
+// lowest incomplete group always resident by the same arguments, none of them waiting on this
+// block — and
 // stores read * rsqrt(mean(read^2) + eps) * weight. The inclusive state is published before
 // that wait, so the chain's successors never wait on the exchange.
 // Every published value is a 64-bit word (value | tag), tag = epoch<<2 | kind, written and
@@ -1113,7 +1115,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     }
   }
 
-  // the last block of the launch re-arms the counters for the next launch (next epoch)
+  // the last block of the launch re-arms the counter for the next launch (next epoch)
   if (threadIdx.x == 0) {
     const unsigned int d = atomicAdd(&hdr->done, 1u);
     if (d == n_tiles - 1) {
@@ -1449,7 +1451,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     }
   }
 
-  // the last block of the launch re-arms the counters for the next launch (next epoch)
+  // the last block of the launch re-arms the counter for the next launch (next epoch)
   if (threadIdx.x == 0) {
     const unsigned int d = atomicAdd(&hdr->done, 1u);
     if (d == n_tiles - 1) {
