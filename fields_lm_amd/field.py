@@ -527,7 +527,8 @@ class IndependentVacancyField(nn.Module):
         GEMM over their weights stacked ([write_proj; gate_proj], a packed copy rebuilt whenever a
         weight or bias changes): raw and gate_pre are column slices of its output, which the scan,
         the decode step and the fused tail read in place (row stride dim + C + dim)."""
-        if not (self.fuse_in_proj and self._no_grad(x)):
+        if not (self.fuse_in_proj and self._no_grad(x)) or self.write_proj.bias is None \
+                or self.gate_proj.bias is None:
             return self.write_proj(x), self.gate_proj(x)
         w, b = self._packed_in_proj()
         y = F.linear(x, w, b)
@@ -536,7 +537,7 @@ class IndependentVacancyField(nn.Module):
 
     def _packed_in_proj(self) -> Tuple[torch.Tensor, torch.Tensor]:
         srcs = (self.write_proj.weight, self.write_proj.bias, self.gate_proj.weight, self.gate_proj.bias)
-        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in srcs)
+        key = tuple((id(t), t.data_ptr(), t._version, t.dtype, t.device) for t in srcs)
         if self._packed is None or self._packed[0] != key:
             with torch.no_grad():
                 w = torch.cat([srcs[0], srcs[2]], 0)
