@@ -292,6 +292,67 @@ struct WaveTile {
     }
   }
 
+  // Gates from bf16 raw staged in LDS: plane p of this wave's row j at s[p*plane + j*64 + lane].
+  __device__ __forceinline__ void load_lds(const bf16_bits* s, int plane, int lane,
+                                           const float* gm) {
+    static_assert(K == 1, "LDS staging holds one channel per lane");
+    const float g9 = kVacancyMax * gm[0];
+#pragma unroll
+    for (int j = 0; j < L; ++j) {
+      const float zr = __uint_as_float((uint32_t)s[j * 64 + lane] << 16);
+      const float zi = __uint_as_float((uint32_t)s[plane + j * 64 + lane] << 16);
+      const float zv = __uint_as_float((uint32_t)s[2 * plane + j * 64 + lane] << 16);
+      gates(zr, zi, zv, g9, gk[j][0], gbr[j][0], gbi[j][0]);
+    }
+  }
+
+  // materialize() for fp32 read through a per-wave LDS region `stage` (4 planes x 4 rows x 64
+  // floats): each group of 4 rows is written to LDS one channel per lane, read back 16 bytes per
+  // lane (4 channels of one row-plane) and stored with 16-byte buffer stores. Rows past the
+  // descriptor's bound are dropped by it; the tile's 64 channels must all lie below C.
+  __device__ __forceinline__ void materialize_lds(rsrc_t w, int lane, int so0, int row_bytes,
+                                                  int plane_bytes, int ch_bytes0, int n,
+                                                  float* stage, const float* lr, const float* li,
+                                                  float* sr, float* si) const {
+    static_assert(K == 1 && L % 4 == 0, "LDS-staged stores: one channel per lane, rows in fours");
+    // (n = valid rows of the wave.) This lane's piece of a 16-byte store: row-plane rp = 4 * i + lane / 16 of instruction i,
+    // channels 4 * (lane % 16) .. + 3
+    const int piece = lane & 15, rp_lane = lane >> 4;
+#pragma unroll
+    for (int g = 0; g < L / 4; ++g) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 4 * g + r;
+        const float mr = lr[0] * sr[0] - li[0] * si[0];
+        const float mi = lr[0] * si[0] + li[0] * sr[0];
+        const float dr = fmaf(-gk[j][0], mr, mr), di = fmaf(-gk[j][0], mi, mi);
+        if (j < n) {  // rows from n on lie past T: their stores are dropped, the state stops here
+          sr[0] = fmaf(gk[j][0], mr, gbr[j][0]);
+          si[0] = fmaf(gk[j][0], mi, gbi[j][0]);
+        }
+        stage[(0 * 4 + r) * 64 + lane] = sr[0];
+        stage[(1 * 4 + r) * 64 + lane] = si[0];
+        stage[(2 * 4 + r) * 64 + lane] = dr;
+        stage[(3 * 4 + r) * 64 + lane] = di;
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int rp = 4 * i + rp_lane, plane = rp >> 2, row = rp & 3;
+        const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
+        u32x4 q;
+        q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
+        q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
+        // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
+        // the compiler's wait states for a VALU overwriting the store's data VGPRs right after
+        // it, and on gfx950 that overwrite reached memory (component 1, the next instruction's
+        // target) for some lanes; with a constant soffset the wait states are inserted
+        __builtin_amdgcn_raw_buffer_store_b128(
+            q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
+            0, 0);
+      }
+    }
+  }
+
   // Summary over all L steps: P = prod(1-v), B = state reached from 0.
   __device__ __forceinline__ void summary(const float* lr, const float* li, float* P, float* Br,
                                           float* Bi) const {
@@ -898,7 +959,11 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
 
 // NORM: out = RMSNorm(read) (canon:300-309 applied to canon:1176-1193's read), norm_w [4C],
 // sib = per-row partials [n_tiles][W*L] words; otherwise out = read and those are unused.
-template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM>
+// LDSIO (bf16 raw, fp32 read, K = 1, every channel tile full, 16-byte aligned raw rows): each
+// wave stages its own raw rows in LDS with 16-byte buffer loads that write LDS directly and
+// forms the gates from there, and stores read through a per-wave LDS transpose with 16-byte
+// stores (the staging region is free again once the look-back's barriers are behind).
+template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
@@ -914,6 +979,11 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   __shared__ float s_carry[2][CT];
   __shared__ int s_meta[4];           // j, n, kind, done
   __shared__ uint32_t s_tk[2];
+  // LDSIO: raw [3][TC][CT] bf16, later the per-wave store staging (W x 4 planes x 4 rows x CT fp32)
+  static_assert(!LDSIO || (K == 1 && L % 8 == 0 && sizeof(RawT) == 2 && sizeof(OutT) == 4 && !NORM),
+                "LDS-staged I/O: bf16 raw, fp32 read, one channel per lane, rows in eights");
+  static_assert(!LDSIO || W * 16 * CT * 4 <= 3 * TC * CT * 2, "store staging exceeds the raw region");
+  __shared__ __align__(16) bf16_bits s_io[LDSIO ? 3 * TC * CT : 8];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -953,7 +1023,21 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
   const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, c0);
   WaveTile<RawT, K, L> tile;
-  tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
+  if constexpr (LDSIO) {
+    // this wave's rows: 8 rows of one plane per instruction (lane = 8 * row + 16-byte piece)
+    const int vo = ctile * CT * (int)sizeof(RawT) + (lane >> 3) * io.raw_row + (lane & 7) * 16;
+#pragma unroll
+    for (int q = 0; q < 6; ++q) {
+      const int plane = q >> 1, r0 = wave * L + (q & 1) * 8;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          io.raw, (__attribute__((address_space(3))) void*)&s_io[(plane * TC + r0) * CT], 16, vo,
+          r0 * io.raw_row + plane * io.raw_plane, 0, 0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the wave reads only the rows it staged itself
+    tile.load_lds(&s_io[wave * L * CT], TC * CT, lane, gm);
+  } else {
+    tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
+  }
   if (in_order && threadIdx.x == 0) s_tk[1] = (uint32_t)(epoch_word >> 32);
   const int n_valid = min(max(T - (t_begin + wave * L), 0), L);
   {
@@ -1102,6 +1186,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
                                            io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
                                            si, scale, nw);
+    } else if constexpr (LDSIO) {
+      float* stage = reinterpret_cast<float*>(s_io) + wave * 16 * CT;
+      tile.materialize_lds(io.read, lane, wave * L * io.read_row, io.read_row, io.read_plane,
+                           ctile * CT * (int)sizeof(OutT), n_valid, stage, lr, li, sr, si);
     } else {
       tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
                                      io.read_plane, n_valid, lr, li, sr, si);
@@ -1881,6 +1969,12 @@ constexpr LookbackTiling kLookbackTilings[] = {
     {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4},  {1, 16, 4, 4},
 };
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
+// The default tiling with LDS-staged raw loads and read stores (LDSIO) is what variant 0 runs for
+// the inputs it takes (bf16 raw, fp32 read, C a multiple of 64, 16-byte aligned rows); variant
+// kLdsIoVariant asks for it explicitly and kRegIoVariant for the default tiling with register
+// loads and stores on every input.
+constexpr int kLdsIoVariant = kNumLookbackTilings;
+constexpr int kRegIoVariant = kNumLookbackTilings + 1;
 // The RMSNorm epilogue runs with the default tiling only; a group of channel tiles must be
 // resident together, so its size n_ctiles = C/64 is capped (C <= 4096).
 constexpr LookbackTiling kNormTiling = kLookbackTilings[0];
@@ -1979,7 +2073,7 @@ struct NormArgs {
   float eps;
 };
 
-template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM>
+template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
                     float* state_out, void* read, void* workspace, NormArgs norm,
@@ -1997,7 +2091,7 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // start, which the look-back needs to keep up (B=1, T=65,536: 155 us; 203 us in block order,
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
-  fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM><<<g.n_tiles, W * 64, 0, stream>>>(
+  fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), reinterpret_cast<LookbackHeader*>(ws),
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
@@ -2158,7 +2252,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   const int variant = algo >> 8;
   if (base_algo != FL_ALGO_AUTO && base_algo != FL_ALGO_CHUNKED3 && base_algo != FL_ALGO_LOOKBACK)
     return FL_ERR_INVALID_ARGUMENT;
-  if (variant < 0 || variant >= kNumLookbackTilings) return FL_ERR_INVALID_ARGUMENT;
+  if (variant < 0 || variant > kRegIoVariant) return FL_ERR_INVALID_ARGUMENT;
   if (B <= 0 || T <= 0 || C <= 0 || B > kMaxB || C > kMaxC || T > kMaxT)
     return FL_ERR_INVALID_ARGUMENT;
   if (raw_stride_t < 3 * C || raw_stride_b < 0) return FL_ERR_INVALID_ARGUMENT;
@@ -2205,9 +2299,20 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
     FL_C3(float, float)
 #undef FL_C3
   }
+  // bf16 raw with 16-byte aligned rows, fp32 read, every 64-channel tile full
+  const bool ldsio_ok = norm.weight == nullptr && raw16 && !out16 && C % 64 == 0 &&
+                        aligned(raw, 16) && raw_stride_t % 8 == 0 &&
+                        (B == 1 || raw_stride_b % 8 == 0) && aligned(read, 16);
+  if ((variant == 0 || variant == kLdsIoVariant) && ldsio_ok) {
+    constexpr LookbackTiling tl = kLookbackTilings[0];
+    return launch_lookback<bf16_bits, float, tl.k, tl.l, tl.w, tl.occ, false, true>(
+        raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, state_out, read,
+        workspace, norm, s);
+  }
+  const int lb_variant = variant >= kLdsIoVariant ? 0 : variant;
 #define FL_LBD(R, O)                                                                          \
-  return dispatch_lookback<R, O>(variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, \
-                                 gamma, state_in, state_out, read, workspace, norm, s);
+  return dispatch_lookback<R, O>(lb_variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr,  \
+                                 ti, gamma, state_in, state_out, read, workspace, norm, s);
   if (raw16 && out16) FL_LBD(bf16_bits, bf16_bits)
   if (raw16) FL_LBD(bf16_bits, float)
   if (out16) FL_LBD(float, bf16_bits)

@@ -36,7 +36,10 @@ extern "C" {
 #define FL_DTYPE_BF16 1
 
 /* algorithm selector for fl_scan_forward_ex (low 8 bits); bits 8.. select a tiling variant of
- * FL_ALGO_LOOKBACK for tuning (0 = default) */
+ * FL_ALGO_LOOKBACK for tuning: 0 = default (LDS-staged 16-byte loads and stores where raw is bf16
+ * with 16-byte aligned rows, read is fp32 and C is a multiple of 64; register loads and stores
+ * otherwise), 1..7 = other tilings, 8 = LDS-staged where possible, 9 = default tiling with
+ * register loads and stores on every input */
 #define FL_ALGO_AUTO 0
 #define FL_ALGO_CHUNKED3 1 /* chunk summary -> chunk carry -> chunk materialise (three launches) */
 #define FL_ALGO_LOOKBACK 2 /* single launch, decoupled look-back across chunks (default) */

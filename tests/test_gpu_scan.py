@@ -69,9 +69,10 @@ def test_scan_matches_oracle(dev, shape, dtype, algo):
     assert torch.isfinite(read).all()
 
 
-@pytest.mark.parametrize("variant", range(8))
+@pytest.mark.parametrize("variant", range(10))
 def test_lookback_tilings(dev, variant):
-    """Every look-back tiling (algo bits 8..) on ragged shapes, fp32 and bf16, with state_in."""
+    """Every look-back tiling (algo bits 8..) on ragged shapes, fp32 and bf16, with state_in
+    (variants 0 and 8 stage the bf16 cases with full channel tiles through LDS, variant 9 never)."""
     from fields_lm_amd import _native as nat
     from fields_lm_amd import field_scan
 
@@ -87,6 +88,35 @@ def test_lookback_tilings(dev, variant):
         exp_read, exp_state = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
         assert oracle.rel_err(read.cpu(), exp_read) <= TOL, (B, T, C)
         assert oracle.rel_err(state.cpu(), exp_state) <= TOL, (B, T, C)
+
+
+def test_lds_staged_io_equals_register_io(dev):
+    """The LDS-staged loads and stores (default for bf16 raw, fp32 read, C % 64 == 0) give the
+    register path's result bit for bit: the same arithmetic in the same order. Ragged T (a
+    partial last chunk, waves with no or some valid rows), B > 1 with padded batch and row
+    strides, state_in, and inputs that do not qualify (C % 64 != 0, an odd row stride) and run
+    the register path under both selectors."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan
+
+    cases = [(3, 1000, 512, 0, 0), (1, 4099, 64, 0, 0), (2, 77, 128, 0, 0), (4, 130, 192, 8, 64),
+             (1, 3, 64, 0, 0), (2, 500, 96, 0, 0), (2, 300, 128, 0, 1)]
+    for (B, T, C, pad_t, pad_b) in cases:
+        print(f"[case] lds staged io B={B} T={T} C={C} pad_t={pad_t} pad_b={pad_b}", flush=True)
+        g = torch.Generator().manual_seed(B * 1000 + T + C)
+        st = 3 * C + pad_t
+        base = (torch.randn(B * (T * st + pad_b), generator=g) * 2).to(torch.bfloat16)
+        raw = base.as_strided((B, T, 3 * C), (T * st + pad_b, st, 1))
+        sin = torch.randn(B, 2 * C, generator=g) * 0.2
+        tr, ti, gamma = _params(C, seed=C + 7)
+        args = [base.to(dev).as_strided(raw.shape, raw.stride())] + _to(dev, tr, ti, gamma)
+        a, sa = field_scan(*args, state_in=sin.to(dev), return_state=True, algo=nat.FL_ALGO_AUTO)
+        b, sb = field_scan(*args, state_in=sin.to(dev), return_state=True,
+                           algo=nat.FL_ALGO_LOOKBACK | (9 << 8))
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(sa, sb), (B, T, C, pad_t, pad_b)
+        exp_read, _ = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
+        assert oracle.rel_err(a.cpu(), exp_read) <= TOL, (B, T, C)
 
 
 def test_workspace_reuse_across_shapes_and_algos(dev):
@@ -228,16 +258,20 @@ def test_empty_and_errors(dev):
         fused_field_read(torch.zeros(1, 4, 3 * (C + 1), device=dev), tr, ti, gamma, 32, 64)
 
 
+@pytest.mark.parametrize("algo", ["auto", "register"])
 @pytest.mark.parametrize("name", ["scan_b8_t2048_d1024", "scan_b1_t65536_d1024"])
-def test_full_size_workloads(dev, name):
-    """Configs 2 and 4 at full size, bf16 raw; config 4 also checks the carry at every
-    2,048-step boundary (32 boundaries) against float64."""
+def test_full_size_workloads(dev, name, algo):
+    """Configs 2 and 4 at full size, bf16 raw (default path, LDS-staged I/O, and the register
+    loads and stores); config 4 also checks the carry at every 2,048-step boundary (32
+    boundaries) against float64."""
+    from fields_lm_amd import _native as nat
     from fields_lm_amd import field_scan
     from fields_lm_amd.workloads import make_scan_workload
 
-    print(f"[case] full size {name}", flush=True)
+    print(f"[case] full size {name} {algo}", flush=True)
     wl = make_scan_workload(name, dev)
-    read, state = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma, return_state=True)
+    code = nat.FL_ALGO_AUTO if algo == "auto" else nat.FL_ALGO_LOOKBACK | (9 << 8)
+    read, state = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma, return_state=True, algo=code)
     torch.cuda.synchronize()
     exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
     got = read.cpu()
