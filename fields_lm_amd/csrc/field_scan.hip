@@ -27,6 +27,12 @@
 
 #include "fields_amd.h"
 
+// 1: the backward kernel stages its second pass's inputs in LDS where the layout allows (the
+// default); 0 keeps register loads everywhere (a build switch for comparisons)
+#ifndef FL_BWD_PREFETCH
+#define FL_BWD_PREFETCH 1
+#endif
+
 namespace {
 
 constexpr float kVacancyMax = 0.9f;  // canon:68 VAC_MAX
@@ -52,6 +58,8 @@ __device__ __forceinline__ int uniform(int x) { return __builtin_amdgcn_readfirs
 // ------------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float raw_value(float x) { return x; }
+__device__ __forceinline__ float raw_value(bf16_bits x) { return __uint_as_float((uint32_t)x << 16); }
 
 // raw: buffer load at (voffset, soffset) bytes
 template <typename RawT, int K>
@@ -1232,8 +1240,11 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 // and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
 // then the waves in order) into per-tile partials that fl_param_grad_{segment,final}_kernel add up over
 // the tiles of each channel in a fixed order (deterministic).
+// PF (K = 1, every channel tile full, 16-byte aligned raw rows): the second pass's inputs (z_r,
+// z_i and s_{t-1}) are staged in LDS by 16-byte buffer loads that write LDS directly, issued
+// with the first pass's loads, so that no load latency follows the look-back.
 // ------------------------------------------------------------------------------------------
-template <typename RawT, typename GradT, int K, int L, int W, int OCC>
+template <typename RawT, typename GradT, int K, int L, int W, int OCC, bool PF = false>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
@@ -1251,6 +1262,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   __shared__ float s_carry[2][CT];
   __shared__ int s_meta[4];
   __shared__ uint32_t s_tk[2];
+  // PF: z_r, z_i [TC][CT] (RawT), then Re s_{t-1}, Im s_{t-1} [TC][CT] (fp32)
+  constexpr int kPfRaw = TC * CT * (int)sizeof(RawT);
+  static_assert(!PF || (K == 1 && L % 8 == 0), "LDS staging: one channel per lane, rows in eights");
+  __shared__ __align__(16) unsigned char s_pf[PF ? 2 * kPfRaw + 2 * TC * CT * 4 : 16];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -1318,6 +1333,44 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 #pragma unroll
     for (int k = 0; k < K; ++k)
       gv[j][k] = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv[k] * -kLog2e));
+  }
+  // s_{t-1} of the tile's rows comes from the forward's read starting one row earlier (from the
+  // tile's own first row for the first tile, whose row before the sequence start is state_in).
+  // Row and row count forced wave-uniform: a descriptor the compiler takes for divergent costs a
+  // readfirstlane loop around every load through it.
+  const bool first = t_begin == 0;
+  const int prev_row = uniform(first ? t_begin : t_begin - 1);
+  const int prev_rows = uniform(first ? rows : rows + 1);
+  const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + prev_row) * 4 * C,
+                                  (uint32_t)((int64_t)prev_rows * 4 * C * 4));
+  if constexpr (PF) {
+    // raw planes: a row of CT channels is kRawLanes 16-byte pieces, kRawRows rows per load
+    constexpr int kRawLanes = CT * (int)sizeof(RawT) / 16, kRawRows = 64 / kRawLanes;
+    const int vo_r = ctile * CT * (int)sizeof(RawT) + (lane / kRawLanes) * raw_row + (lane % kRawLanes) * 16;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int i = 0; i < L / kRawRows; ++i) {
+        const int r0 = wave * L + i * kRawRows;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r_raw, (__attribute__((address_space(3))) void*)&s_pf[p * kPfRaw + r0 * CT * (int)sizeof(RawT)],
+            16, vo_r, r0 * raw_row + p * raw_plane, 0, 0);
+      }
+    // s planes: 4 rows of 64 fp32 per load; row r of the tile reads row r - first of r_prev, and
+    // the first tile's row 0 (before the sequence start) an out-of-range offset (state_in later)
+    const int vo_s = ctile * CT * 4 + (lane & 15) * 16;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int i = 0; i < L / 4; ++i) {
+        const int r0 = wave * L + 4 * i;
+        const bool head = first && r0 == 0;
+        const int q = lane >> 4;
+        const int vo = head ? (q == 0 ? 0x7fffffff : vo_s + (q - 1) * grd_row) : vo_s + q * grd_row;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(
+            r_prev, (__attribute__((address_space(3))) void*)&s_pf[2 * kPfRaw + (p * TC + r0) * CT * 4],
+            16, vo, head ? p * f_plane : (r0 - (first ? 1 : 0)) * grd_row + p * f_plane, 0, 0);
+      }
   }
   if (in_order && threadIdx.x == 0) s_tk[1] = (uint32_t)(epoch_word >> 32);
   {
@@ -1450,21 +1503,28 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     // state_in.
     float zr[L][K], zi[L][K], pr[L][K], pi[L][K];
     {
-      const bool first = t_begin == 0;
-      // row and row count forced wave-uniform: a descriptor the compiler takes for divergent
-      // costs a readfirstlane loop around every load through it
-      const int prev_row = uniform(first ? t_begin : t_begin - 1);
-      const int prev_rows = uniform(first ? rows : rows + 1);
-      const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + prev_row) * 4 * C,
-                                      (uint32_t)((int64_t)prev_rows * 4 * C * 4));
+      if constexpr (PF) {
+        __builtin_amdgcn_s_waitcnt(0);  // the wave reads only the rows it staged itself
+        const RawT* szr = reinterpret_cast<const RawT*>(s_pf);
+        const float* sp = reinterpret_cast<const float*>(s_pf + 2 * kPfRaw);
 #pragma unroll
-      for (int j = 0; j < L; ++j) {
-        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
-        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi[j]);
-        const int prow = wave * L + j - (first ? 1 : 0);
-        const int so = prow >= 0 ? prow * grd_row : 0x7fffffff;
-        RawLoad<float, K>::run(r_prev, vo_f, so, pr[j]);
-        RawLoad<float, K>::run(r_prev, vo_f, so == 0x7fffffff ? so : so + f_plane, pi[j]);
+        for (int j = 0; j < L; ++j) {
+          const int x = (wave * L + j) * CT + lane;
+          zr[j][0] = raw_value(szr[x]);
+          zi[j][0] = raw_value(szr[TC * CT + x]);
+          pr[j][0] = sp[x];
+          pi[j][0] = sp[TC * CT + x];
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < L; ++j) {
+          RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
+          RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi[j]);
+          const int prow = wave * L + j - (first ? 1 : 0);
+          const int so = prow >= 0 ? prow * grd_row : 0x7fffffff;
+          RawLoad<float, K>::run(r_prev, vo_f, so, pr[j]);
+          RawLoad<float, K>::run(r_prev, vo_f, so == 0x7fffffff ? so : so + f_plane, pi[j]);
+        }
       }
       if (w0 == 0) {
 #pragma unroll
@@ -2211,11 +2271,22 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // ticket order as in the forward launch: block order for short chains, one counter otherwise
   const bool in_order = g.n_chunks <= 64;
   float* pgrad = reinterpret_cast<float*>(ws + lay.pgrad_off);
-  fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ><<<g.n_tiles, tl.w * 64, 0, stream>>>(
-      static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma,
-      state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad,
-      reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
-      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, (uint32_t)n_chains, in_order);
+  // LDS-staged second-pass inputs: every channel tile full, raw rows and read 16-byte aligned
+  const int64_t esz = (int64_t)sizeof(RawT);
+  const bool pf = FL_BWD_PREFETCH && C % CT == 0 && aligned(raw, 16) && (st * esz) % 16 == 0 &&
+                  (B == 1 || (sb * esz) % 16 == 0) && aligned(read, 16);
+#define FL_BWK(PF)                                                                               \
+  fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ, PF><<<g.n_tiles, tl.w * 64, 0, stream>>>( \
+      static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma, \
+      state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad, \
+      reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),  \
+      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, (uint32_t)n_chains, in_order)
+  if (pf) {
+    FL_BWK(true);
+  } else {
+    FL_BWK(false);
+  }
+#undef FL_BWK
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return hip_status(e);
   float* seg = reinterpret_cast<float*>(ws + lay.seg_off);

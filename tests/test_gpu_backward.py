@@ -210,6 +210,38 @@ def test_field_block_training_gradients(dev):
         assert oracle.rel_err(got[k], p.grad) <= 2e-4, k
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_backward_lds_staged_equals_register_loads(dev, dtype):
+    """The second pass's inputs staged in LDS (every channel tile full, 16-byte aligned raw rows)
+    and loaded into registers (the same values in raw rows with an odd stride) give identical
+    gradients: the same arithmetic in the same order. Ragged T (partial last tile), the first tile
+    (its row before the sequence start comes from state_in), B > 1, and more than 64 chunks."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    for (B, T, C) in [(3, 1000, 512), (2, 77, 128), (1, 4099, 64), (2, 8, 64), (4, 130, 192)]:
+        print(f"[case] backward lds staged B={B} T={T} C={C} {dtype}", flush=True)
+        g = torch.Generator().manual_seed(B * 100 + T + C)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype)
+        tr, ti, gamma = _params(C, seed=C + 3)
+        sin = torch.randn(B, 2 * C, generator=g) * 0.3
+        gread = torch.randn(B, T, 4 * C, generator=g)
+        gso = torch.randn(B, 2 * C, generator=g)
+        d = [t.to(dev) for t in (raw, tr, ti, gamma, sin, gread, gso)]
+        odd = torch.zeros(B, T, 3 * C + 1, device=dev, dtype=dtype)[..., :3 * C]
+        odd.copy_(d[0])
+        read = field_scan(d[0], d[1], d[2], d[3], state_in=d[4])
+        a = field_scan_backward(d[0], d[1], d[2], d[3], read, d[5], state_in=d[4], grad_state_out=d[6],
+                                return_state_grad=True)
+        b = field_scan_backward(odd, d[1], d[2], d[3], read, d[5], state_in=d[4], grad_state_out=d[6],
+                                return_state_grad=True)
+        torch.cuda.synchronize()
+        for x, y in zip(a, b):
+            assert torch.equal(x, y), (B, T, C)
+        e_raw = _oracle_grads(raw.float(), tr, ti, gamma, gread, sin, gso)[0]
+        tol_raw = TOL if dtype == torch.float32 else 4e-3
+        assert oracle.rel_err(a[0].float().cpu(), e_raw) <= tol_raw
+
+
 def test_backward_workspace_reuse_across_shapes(dev):
     """One backward workspace (the per-stream cache), calls alternating shape: the parameter
     gradients of every call equal those of the shape's first call bit for bit (the reduction's
