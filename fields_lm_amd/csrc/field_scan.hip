@@ -314,18 +314,18 @@ struct WaveTile {
     }
   }
 
-  // materialize() for fp32 read through a per-wave LDS region `stage` (4 planes x 4 rows x 64
-  // floats): each group of 4 rows is written to LDS one channel per lane, read back 16 bytes per
-  // lane (4 channels of one row-plane) and stored with 16-byte buffer stores. Rows past the
-  // descriptor's bound are dropped by it; the tile's 64 channels must all lie below C.
+  // materialize() (NORM: materialize_norm()) through a per-wave LDS region `stage` (4 planes x
+  // 4 rows x 64 floats): each group of 4 rows is written to LDS one channel per lane, read back
+  // as 16 bytes of output per lane (4 fp32 or 8 bf16 channels of one row-plane) and stored with
+  // 16-byte buffer stores. The whole store offset is in voffset, so rows past the descriptor's
+  // bound (past T) are dropped by it; the tile's 64 channels must all lie below C.
+  template <typename OutT, bool NORM>
   __device__ __forceinline__ void materialize_lds(rsrc_t w, int lane, int so0, int row_bytes,
                                                   int plane_bytes, int ch_bytes0, int n,
                                                   float* stage, const float* lr, const float* li,
-                                                  float* sr, float* si) const {
+                                                  float* sr, float* si, float scale,
+                                                  const float (*nw)[K]) const {
     static_assert(K == 1 && L % 4 == 0, "LDS-staged stores: one channel per lane, rows in fours");
-    // (n = valid rows of the wave.) This lane's piece of a 16-byte store: row-plane rp = 4 * i + lane / 16 of instruction i,
-    // channels 4 * (lane % 16) .. + 3
-    const int piece = lane & 15, rp_lane = lane >> 4;
 #pragma unroll
     for (int g = 0; g < L / 4; ++g) {
 #pragma unroll
@@ -333,30 +333,54 @@ struct WaveTile {
         const int j = 4 * g + r;
         const float mr = lr[0] * sr[0] - li[0] * si[0];
         const float mi = lr[0] * si[0] + li[0] * sr[0];
-        const float dr = fmaf(-gk[j][0], mr, mr), di = fmaf(-gk[j][0], mi, mi);
+        float o[4];
+        o[2] = fmaf(-gk[j][0], mr, mr);
+        o[3] = fmaf(-gk[j][0], mi, mi);
         if (j < n) {  // rows from n on lie past T: their stores are dropped, the state stops here
           sr[0] = fmaf(gk[j][0], mr, gbr[j][0]);
           si[0] = fmaf(gk[j][0], mi, gbi[j][0]);
         }
-        stage[(0 * 4 + r) * 64 + lane] = sr[0];
-        stage[(1 * 4 + r) * 64 + lane] = si[0];
-        stage[(2 * 4 + r) * 64 + lane] = dr;
-        stage[(3 * 4 + r) * 64 + lane] = di;
-      }
+        o[0] = sr[0];
+        o[1] = si[0];
+        if constexpr (NORM) {
+          const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), j));
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int rp = 4 * i + rp_lane, plane = rp >> 2, row = rp & 3;
-        const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
-        u32x4 q;
-        q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
-        q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
-        // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
-        // the compiler's wait states for a VALU overwriting the store's data VGPRs right after
-        // it, and on gfx950 that overwrite reached memory (component 1, the next instruction's
-        // target) for some lanes; with a constant soffset the wait states are inserted
-        __builtin_amdgcn_raw_buffer_store_b128(
-            q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
-            0, 0);
+          for (int p = 0; p < 4; ++p) o[p] = (o[p] * sc) * nw[p][0];
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) stage[(p * 4 + r) * 64 + lane] = o[p];
+      }
+      // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
+      // the compiler's wait states for a VALU op overwriting the store's data VGPRs right after
+      // it, and on gfx950 that overwrite reached memory (component 1, the next instruction's
+      // target) for some lanes; with a constant soffset the wait states are inserted
+      if constexpr (sizeof(OutT) == 4) {
+        // row-plane rp = 4 * i + lane / 16 of instruction i, channels 4 * (lane % 16) .. + 3
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int rp = 4 * i + (lane >> 4), plane = rp >> 2, row = rp & 3, piece = lane & 15;
+          const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
+          u32x4 q;
+          q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
+          q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
+              0, 0);
+        }
+      } else {
+        // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int rp = 8 * i + (lane >> 3), plane = rp >> 2, row = rp & 3, piece = lane & 7;
+          const float4 a = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece);
+          const float4 c = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece + 4);
+          u32x4 q;
+          q.x = bf16_pair(a.x, a.y); q.y = bf16_pair(a.z, a.w);
+          q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
+          __builtin_amdgcn_raw_buffer_store_b128(
+              q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
+              0, 0);
+        }
       }
     }
   }
@@ -988,8 +1012,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   __shared__ int s_meta[4];           // j, n, kind, done
   __shared__ uint32_t s_tk[2];
   // LDSIO: raw [3][TC][CT] bf16, later the per-wave store staging (W x 4 planes x 4 rows x CT fp32)
-  static_assert(!LDSIO || (K == 1 && L % 8 == 0 && sizeof(RawT) == 2 && sizeof(OutT) == 4 && !NORM),
-                "LDS-staged I/O: bf16 raw, fp32 read, one channel per lane, rows in eights");
+  static_assert(!LDSIO || (K == 1 && L % 8 == 0 && sizeof(RawT) == 2),
+                "LDS-staged I/O: bf16 raw, one channel per lane, rows in eights");
   static_assert(!LDSIO || W * 16 * CT * 4 <= 3 * TC * CT * 2, "store staging exceeds the raw region");
   __shared__ __align__(16) bf16_bits s_io[LDSIO ? 3 * TC * CT : 8];
 
@@ -1191,13 +1215,21 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       for (int m = L; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
       if (__ballot(sib_failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
       const float scale = rsqrtf(fmaf(tot, inv_n, eps));
-      tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
-                                           io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
-                                           si, scale, nw);
+      if constexpr (LDSIO) {
+        float* stage = reinterpret_cast<float*>(s_io) + wave * 16 * CT;
+        tile.template materialize_lds<OutT, true>(io.read, lane, wave * L * io.read_row, io.read_row,
+                                                  io.read_plane, ctile * CT * (int)sizeof(OutT),
+                                                  n_valid, stage, lr, li, sr, si, scale, nw);
+      } else {
+        tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
+                                             io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
+                                             si, scale, nw);
+      }
     } else if constexpr (LDSIO) {
       float* stage = reinterpret_cast<float*>(s_io) + wave * 16 * CT;
-      tile.materialize_lds(io.read, lane, wave * L * io.read_row, io.read_row, io.read_plane,
-                           ctile * CT * (int)sizeof(OutT), n_valid, stage, lr, li, sr, si);
+      tile.template materialize_lds<OutT, false>(io.read, lane, wave * L * io.read_row, io.read_row,
+                                                 io.read_plane, ctile * CT * (int)sizeof(OutT),
+                                                 n_valid, stage, lr, li, sr, si, 0.f, nullptr);
     } else {
       tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
                                      io.read_plane, n_valid, lr, li, sr, si);
@@ -2370,15 +2402,25 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
     FL_C3(float, float)
 #undef FL_C3
   }
-  // bf16 raw with 16-byte aligned rows, fp32 read, every 64-channel tile full
-  const bool ldsio_ok = norm.weight == nullptr && raw16 && !out16 && C % 64 == 0 &&
-                        aligned(raw, 16) && raw_stride_t % 8 == 0 &&
+  // LDS-staged I/O: bf16 raw with 16-byte aligned rows, every 64-channel tile full, read (fp32
+  // or bf16, with or without the RMSNorm epilogue) 16-byte aligned
+  const bool ldsio_ok = raw16 && C % 64 == 0 && aligned(raw, 16) && raw_stride_t % 8 == 0 &&
                         (B == 1 || raw_stride_b % 8 == 0) && aligned(read, 16);
   if ((variant == 0 || variant == kLdsIoVariant) && ldsio_ok) {
     constexpr LookbackTiling tl = kLookbackTilings[0];
-    return launch_lookback<bf16_bits, float, tl.k, tl.l, tl.w, tl.occ, false, true>(
-        raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, state_out, read,
-        workspace, norm, s);
+    static_assert(tl.k == kNormTiling.k && tl.l == kNormTiling.l && tl.w == kNormTiling.w,
+                  "the RMSNorm epilogue runs with the default tiling");
+#define FL_LDSIO(O, N)                                                                          \
+  return launch_lookback<bf16_bits, O, tl.k, tl.l, tl.w, tl.occ, N, true>(                      \
+      raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, state_out, read,        \
+      workspace, norm, s);
+    if (norm.weight != nullptr) {
+      if (out16) { FL_LDSIO(bf16_bits, true) }
+      FL_LDSIO(float, true)
+    }
+    if (out16) { FL_LDSIO(bf16_bits, false) }
+    FL_LDSIO(float, false)
+#undef FL_LDSIO
   }
   const int lb_variant = variant >= kLdsIoVariant ? 0 : variant;
 #define FL_LBD(R, O)                                                                          \

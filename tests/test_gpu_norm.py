@@ -101,6 +101,33 @@ def test_norm_bf16_out_is_rounded_fp32_out(dev):
         torch.testing.assert_close(s32, s_plain, rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_norm_lds_staged_equals_register_io(dev, out_dtype):
+    """The epilogue's LDS-staged 16-byte loads and stores (bf16 raw with 16-byte aligned rows,
+    C % 64 == 0) give the register path's output bit for bit: the same values in raw rows with
+    an odd stride take the register loads and stores. Ragged T, B > 1, the maximum channel count
+    and a chain of more than 64 chunks."""
+    from fields_lm_amd import field_scan_norm
+
+    for (B, T, C) in [(3, 1000, 512), (2, 77, 128), (1, 300, 4096), (2, 9000, 64)]:
+        print(f"[case] scan_norm lds staged B={B} T={T} C={C} {out_dtype}", flush=True)
+        g = torch.Generator().manual_seed(B + T + C + 5)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+        sin = torch.randn(B, 2 * C, generator=g) * 0.2
+        draw, tr, ti, gamma, w = _to(dev, raw, *_params(C, seed=C), _weight(C, C))
+        odd = torch.zeros(B, T, 3 * C + 1, device=dev, dtype=torch.bfloat16)[..., :3 * C]
+        odd.copy_(draw)
+        a, sa = field_scan_norm(draw, tr, ti, gamma, w, state_in=sin.to(dev), return_state=True,
+                                out_dtype=out_dtype)
+        b, sb = field_scan_norm(odd, tr, ti, gamma, w, state_in=sin.to(dev), return_state=True,
+                                out_dtype=out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(sa, sb), (B, T, C)
+        exp_read, _ = oracle.scan_f64(raw.float(), *_params(C, seed=C), state_in=sin)
+        exp = oracle.rms_norm_f64(exp_read, _weight(C, C), 1e-6)
+        assert oracle.rel_err(a.float().cpu(), exp) <= (TOL if out_dtype == torch.float32 else 4e-3)
+
+
 def test_norm_equals_rmsnorm_module_of_read(dev):
     """Fused epilogue == the package's RMSNorm module applied to the plain scan's fp32 read."""
     from fields_lm_amd import RMSNorm, field_scan, field_scan_norm

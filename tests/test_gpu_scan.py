@@ -91,8 +91,8 @@ def test_lookback_tilings(dev, variant):
 
 
 def test_lds_staged_io_equals_register_io(dev):
-    """The LDS-staged loads and stores (default for bf16 raw, fp32 read, C % 64 == 0) give the
-    register path's result bit for bit: the same arithmetic in the same order. Ragged T (a
+    """The LDS-staged loads and stores (default for bf16 raw and C % 64 == 0, fp32 and bf16 read)
+    give the register path's result bit for bit: the same arithmetic in the same order. Ragged T (a
     partial last chunk, waves with no or some valid rows), B > 1 with padded batch and row
     strides, state_in, and inputs that do not qualify (C % 64 != 0, an odd row stride) and run
     the register path under both selectors."""
@@ -110,13 +110,16 @@ def test_lds_staged_io_equals_register_io(dev):
         sin = torch.randn(B, 2 * C, generator=g) * 0.2
         tr, ti, gamma = _params(C, seed=C + 7)
         args = [base.to(dev).as_strided(raw.shape, raw.stride())] + _to(dev, tr, ti, gamma)
-        a, sa = field_scan(*args, state_in=sin.to(dev), return_state=True, algo=nat.FL_ALGO_AUTO)
-        b, sb = field_scan(*args, state_in=sin.to(dev), return_state=True,
-                           algo=nat.FL_ALGO_LOOKBACK | (9 << 8))
-        torch.cuda.synchronize()
-        assert torch.equal(a, b) and torch.equal(sa, sb), (B, T, C, pad_t, pad_b)
-        exp_read, _ = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
-        assert oracle.rel_err(a.cpu(), exp_read) <= TOL, (B, T, C)
+        for rd in (torch.float32, torch.bfloat16):
+            a, sa = field_scan(*args, state_in=sin.to(dev), return_state=True, algo=nat.FL_ALGO_AUTO,
+                               read_dtype=rd)
+            b, sb = field_scan(*args, state_in=sin.to(dev), return_state=True,
+                               algo=nat.FL_ALGO_LOOKBACK | (9 << 8), read_dtype=rd)
+            torch.cuda.synchronize()
+            assert torch.equal(a, b) and torch.equal(sa, sb), (B, T, C, pad_t, pad_b, rd)
+            if rd == torch.float32:
+                exp_read, _ = oracle.scan_f64(raw.float(), tr, ti, gamma, state_in=sin)
+                assert oracle.rel_err(a.cpu(), exp_read) <= TOL, (B, T, C)
 
 
 def test_workspace_reuse_across_shapes_and_algos(dev):
