@@ -31,6 +31,7 @@ if str(REPO) not in sys.path:
     sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBS = 8000.0
+BWD_WAVE_ROWS = 8  # steps per wave of the backward kernel: one stored state read per wave
 METRIC = "Field scan tokens/s + % HBM peak (B8 T2048 d1024); decode tok/s at B64"
 
 
@@ -275,8 +276,9 @@ def decode_comparison(batch: int = 64, dim: int = 1024, prompt: int = 2048, toke
 
 def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
     """fl_scan_backward on a workload (bf16 raw and bf16 grad_raw, fp32 read / grad_read):
-    algorithmic bytes per token 3C*2 (raw) + 4C*4 (grad_read) + 2C*4 (the read's state planes)
-    + 3C*2 (grad_raw) = 18,432 at C = 512."""
+    algorithmic bytes per token 3C*2 (raw) + 4C*4 (grad_read) + 3C*2 (grad_raw) + 2C*4/8 (the
+    read's state at the row before each 8-step wave, from which the kernel recomputes s_{t-1})
+    = 14,848 at C = 512."""
     import torch
 
     from fields_lm_amd import _native as nat
@@ -306,7 +308,7 @@ def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
             nat.check(lib.fl_scan_backward(*args), "fl_scan_backward")
 
     _, ev = time_plan(_Plan(), steps, warmup)
-    nbytes = (3 * C * 2 + 4 * C * 4 + 2 * C * 4 + 3 * C * 2) * B * T
+    nbytes = (3 * C * 2 + 4 * C * 4 + 3 * C * 2 + 2 * C * 4 // BWD_WAVE_ROWS) * B * T
     if nat.workspace_error(ws) != 0:
         raise RuntimeError("backward look-back wait gave up")
     return {"workload": workload, "us_per_step": ev * 1e3, "tokens_per_s": B * T / (ev * 1e-3),

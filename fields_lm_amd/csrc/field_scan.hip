@@ -763,10 +763,10 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // a lower index, so that tile is always resident. A tile
 //   1. loads its raw tile into registers and forms the gates;
 //   2. composes its summary (P, B) and publishes it (status AGG);
-//   3. looks back over its chain: the summaries of earlier tiles are composed until a tile
-//      with a published inclusive state (status INCL) is found, which gives the carry-in; all
-//      W waves fetch and compose predecessor summaries in parallel, up to kLookbackPerWave each
-//      per round;
+//   3. looks back over its chain for the nearest tile with a published inclusive state (status
+//      INCL); the summaries of the tiles after it are fetched by all W waves in parallel and
+//      applied to it one by one, which gives the carry-in (the same values whichever tile's
+//      inclusive state was found: see lookback_carry);
 //   4. publishes its inclusive state (status INCL) and materialises.
 // With the RMSNorm epilogue (NORM), step 4 first runs the tile's recurrence once more without
 // storing, to form each row's partial sum of squares over the tile's channels; publishes the
@@ -803,7 +803,9 @@ constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
 constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
-constexpr int kLookbackPerWave = 8;  // predecessor summaries composed per wave per round
+// Look-back window: the predecessors whose summaries one round stages in LDS (3 x CT floats
+// each): 8W/K, at most 64 (one status load)
+constexpr int lookback_window(int K, int W) { return 8 * W / K < 64 ? 8 * W / K : 64; }
 // data planes of a tile: P, Br, Bi (summary), Sr, Si (inclusive state)
 constexpr int kPlanes = 5;
 
@@ -834,73 +836,68 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
   }
 }
 
-// Decoupled look-back of one tile, run by all W waves of the block: composes the published
-// summaries (AGG) of the tile's predecessors ord-1, ord-2, ... in its chain until one with a
-// published inclusive state (INCL) is found. Every predecessor is a full tile, so its map is
-// A = lamT * P. On return wave 0 holds the tile's carry-in in (cr, ci) (unchanged if a wait gave
-// up, with the error bit set). ``ord`` is the tile's position in its chain's processing order.
-template <int K, int W>
+// Decoupled look-back of one tile, run by all W waves of the block, with a carry that does not
+// depend on timing. The carry is the nearest published inclusive state (INCL) of predecessor
+// j0-n (j0 = ord-1) with the summaries (AGG) of predecessors j0-n+1 .. j0 applied to it one by
+// one, farthest first, by apply_map with A = lamT * P: exactly how each of those predecessors
+// forms its own inclusive state from its carry. Whichever predecessor's inclusive state is found,
+// the carry is therefore the same float values (the predecessor j0's inclusive state, bit for
+// bit). The n summaries are fetched by all W waves in parallel into s_pred (LDS, kWin x 3 x CT
+// floats, nearest first) and applied by wave 0. A tile whose kWin nearest predecessors hold no
+// inclusive state, or one whose nearest non-summary predecessor has published nothing yet, waits
+// and scans again (an inclusive state reaches every tile within kWin of the lowest unfinished
+// one, whose own predecessor is finished). On return wave 0 holds the carry-in in (cr, ci)
+// (unchanged if a wait gave up, with the error bit set). ``ord`` is the tile's position in its
+// chain's processing order; every predecessor is a full tile.
+template <int K, int W, int kWin>
 __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks, const uint32_t* st_chain,
                                                uint64_t* data, uint32_t tag_agg, uint32_t tag_incl,
                                                const float* lTr, const float* lTi, bool ok, int lane,
-                                               int wave, LookbackHeader* hdr,
-                                               float (&s_part)[W][4][64 * K],
+                                               int wave, LookbackHeader* hdr, float* s_pred,
                                                float (&s_carry)[2][64 * K], int (&s_meta)[4],
                                                float* cr, float* ci) {
   constexpr int CT = 64 * K;
-  constexpr int kMaxRound = W * kLookbackPerWave < 64 ? W * kLookbackPerWave : 64;
-  // acc (wave 0): map from the end of the farthest consumed predecessor to the tile start
-  float aAr[K], aAi[K], aBr[K], aBi[K];
-#pragma unroll
-  for (int k = 0; k < K; ++k) { aAr[k] = 1.f; aAi[k] = 0.f; aBr[k] = 0.f; aBi[k] = 0.f; }
+  static_assert(kWin >= 1 && kWin <= 64, "look-back window of one status load");
   uint32_t spins = 0;
   bool failed = false;
-  // Status scan (wave 0): statuses of the 64 predecessors j, j-1, ... in one load; s_meta gets
-  // (j, n, kind): the next round composes the n nearest summaries, then, for kind 2, starts
-  // from the inclusive state of predecessor j-n.
-  auto scan_status = [&](int j) {
-    const int p = j - lane;
+  const int j0 = ord - 1;
+  // Status scan (wave 0): statuses of predecessors j0, j0-1, ..., j0-kWin+1 in one load; s_meta
+  // gets (n, ready): ready when j0 .. j0-n+1 have published summaries and j0-n its inclusive state.
+  auto scan_status = [&]() {
+    const int p = j0 - lane;
+    const bool in_win = lane < kWin && p >= 0;
     uint32_t s = 0;
-    if (p >= 0) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned long long not_agg = __ballot(!(p >= 0 && s == tag_agg));
-    const int i0 = not_agg ? (__ffsll((long long)not_agg) - 1) : 64;
-    int kind;  // 0: first non-summary predecessor not ready, 1: round limit, 2: INCL at j-n
-    int n;
-    if (i0 >= kMaxRound) {
-      n = kMaxRound;
-      kind = 1;
-    } else {
-      n = i0;
+    if (in_win) s = __hip_atomic_load(st_chain + p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned long long not_agg = __ballot(!(in_win && s == tag_agg));
+    int n = 0, ready = 0;
+    if (not_agg != 0ull) {
+      const int i0 = __ffsll((long long)not_agg) - 1;
       const uint32_t s_at = __shfl(s, i0);
-      const int p_at = __shfl(p, i0);
-      kind = (p_at >= 0 && s_at == tag_incl) ? 2 : 0;
+      n = i0;
+      ready = (i0 < kWin && j0 - i0 >= 0 && s_at == tag_incl) ? 1 : 0;
     }
-    if (lane == 0) { s_meta[0] = j; s_meta[1] = n; s_meta[2] = kind; }
+    if (lane == 0) { s_meta[0] = n; s_meta[1] = ready; }
   };
   if (wave == 0) {
-    scan_status(ord - 1);
-    if (lane == 0) s_meta[3] = 0;
+    scan_status();
+    if (lane == 0) { s_meta[2] = 0; s_meta[3] = 0; }
   }
-  // Each round: barrier, every wave composes its share of the n summaries, barrier, wave 0
-  // folds the shares into acc and scans the statuses for the next round.
+  // Each round: barrier, (ready) every wave stages its share of the n summaries and the last wave
+  // the inclusive state, barrier, wave 0 applies them or scans the statuses again.
   while (true) {
     __syncthreads();
     if (s_meta[3]) break;
-    const int jj = s_meta[0], n = s_meta[1], kind = s_meta[2];
-    // this wave composes predecessors jj - i for i in [lo, hi), nearest first
-    const int m = (n + W - 1) / W;
-    const int lo = min(wave * m, n), hi = min(lo + m, n);
-    {
-      float pAr[K], pAi[K], pBr[K], pBi[K];
-#pragma unroll
-      for (int k = 0; k < K; ++k) { pAr[k] = 1.f; pAi[k] = 0.f; pBr[k] = 0.f; pBi[k] = 0.f; }
+    const int n = s_meta[0], ready = s_meta[1];
+    if (ready) {
+      const int m = (n + W - 1) / W;
+      const int lo = min(wave * m, n), hi = min(lo + m, n);
       // sub-batches of kLookbackBatch predecessors, nearest first (no barrier in between)
       for (int q0 = lo; ok && q0 < hi && !failed; q0 += kLookbackBatch) {
         uint64_t w[kLookbackBatch][3][K];
 #pragma unroll
         for (int q = 0; q < kLookbackBatch; ++q) {
           if (q0 + q < hi) {
-            uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
+            uint64_t* dp = data + ((size_t)chain * n_chunks + (j0 - q0 - q)) * kPlanes * CT + lane * K;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
               w[q][0][k] = get_word(dp + k);
@@ -912,78 +909,60 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
 #pragma unroll
         for (int q = 0; q < kLookbackBatch; ++q) {
           if (q0 + q < hi && !failed) {
-            uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - q0 - q)) * kPlanes * CT + lane * K;
+            uint64_t* dp = data + ((size_t)chain * n_chunks + (j0 - q0 - q)) * kPlanes * CT + lane * K;
+            float* sp = s_pred + (size_t)(q0 + q) * 3 * CT + lane * K;
 #pragma unroll
             for (int k = 0; k < K; ++k) {
               uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
               if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins)) { failed = true; break; }
-              // partial <- partial o M(pred), with A(pred) = lam^TC * P
-              const float P = word_value(ww[0]);
-              const float ar = P * lTr[k], ai = P * lTi[k];
-              const float qBr = word_value(ww[1]), qBi = word_value(ww[2]);
-              const float nBr = pAr[k] * qBr - pAi[k] * qBi + pBr[k];
-              const float nBi = pAr[k] * qBi + pAi[k] * qBr + pBi[k];
-              const float nAr = pAr[k] * ar - pAi[k] * ai;
-              const float nAi = pAr[k] * ai + pAi[k] * ar;
-              pAr[k] = nAr; pAi[k] = nAi; pBr[k] = nBr; pBi[k] = nBi;
+              sp[k] = word_value(ww[0]);
+              sp[CT + k] = word_value(ww[1]);
+              sp[2 * CT + k] = word_value(ww[2]);
             }
           }
         }
       }
+      if (wave == W - 1 && ok) {  // inclusive state of predecessor j0 - n
+        uint64_t* dp = data + ((size_t)chain * n_chunks + (j0 - n)) * kPlanes * CT + lane * K;
 #pragma unroll
-      for (int k = 0; k < K; ++k) {
-        s_part[wave][0][lane * K + k] = pAr[k];
-        s_part[wave][1][lane * K + k] = pAi[k];
-        s_part[wave][2][lane * K + k] = pBr[k];
-        s_part[wave][3][lane * K + k] = pBi[k];
+        for (int k = 0; k < K; ++k) {
+          uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
+          if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
+          s_carry[0][lane * K + k] = word_value(ww[0]);
+          s_carry[1][lane * K + k] = word_value(ww[1]);
+        }
       }
     }
-    if (kind == 2 && wave == W - 1 && ok) {  // inclusive state of predecessor jj - n
-      uint64_t* dp = data + ((size_t)chain * n_chunks + (jj - n)) * kPlanes * CT + lane * K;
-#pragma unroll
-      for (int k = 0; k < K; ++k) {
-        uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
-        if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
-        s_carry[0][lane * K + k] = word_value(ww[0]);
-        s_carry[1][lane * K + k] = word_value(ww[1]);
-      }
+    if (__ballot(failed) != 0ull && lane == 0) {
+      atomicOr(&hdr->error, 1u);
+      s_meta[2] = 1;
     }
-    if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
     __syncthreads();
     if (wave == 0) {
-      // acc <- acc o part_0 o part_1 o ...  (part_u covers nearer predecessors than part_u+1)
-      for (int u = 0; u < W; ++u) {
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int x = lane * K + k;
-          const float qAr = s_part[u][0][x], qAi = s_part[u][1][x];
-          const float qBr = s_part[u][2][x], qBi = s_part[u][3][x];
-          const float nBr = aAr[k] * qBr - aAi[k] * qBi + aBr[k];
-          const float nBi = aAr[k] * qBi + aAi[k] * qBr + aBi[k];
-          const float nAr = aAr[k] * qAr - aAi[k] * qAi;
-          const float nAi = aAr[k] * qAi + aAi[k] * qAr;
-          aAr[k] = nAr; aAi[k] = nAi; aBr[k] = nBr; aBi[k] = nBi;
-        }
-      }
       int done = 0;
-      if (kind == 2) {
+      if (s_meta[2]) {
+        done = 1;  // a wait gave up: the carry stays state_in / 0
+      } else if (ready) {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           const int x = lane * K + k;
-          const float sr = s_carry[0][x], si = s_carry[1][x];
-          cr[k] = aAr[k] * sr - aAi[k] * si + aBr[k];
-          ci[k] = aAr[k] * si + aAi[k] * sr + aBi[k];
+          float sr = s_carry[0][x], si = s_carry[1][x];
+          for (int i = n - 1; i >= 0; --i) {
+            const float* sp = s_pred + (size_t)i * 3 * CT + x;
+            apply_map(lTr[k], lTi[k], sp[0], sp[CT], sp[2 * CT], sr, si);
+          }
+          cr[k] = sr;
+          ci[k] = si;
         }
         done = 1;
-      } else if (kind == 0) {
+      } else {
         if (++spins > kSpinLimit) {
-          failed = true;
+          done = 1;
           if (lane == 0) atomicOr(&hdr->error, 1u);
         }
         __builtin_amdgcn_s_sleep(2);
       }
-      if (__ballot(failed) != 0ull) done = 1;  // give up: the carry stays state_in / 0
-      if (!done) scan_status(jj - n);
+      if (!done) scan_status();
       if (lane == 0) s_meta[3] = done;
     }
   }
@@ -1006,16 +985,21 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
+  constexpr int kWin = lookback_window(K, W);
   __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
-  __shared__ float s_part[W][4][CT];  // look-back partial maps (Ar, Ai, Br, Bi)
   __shared__ float s_carry[2][CT];
-  __shared__ int s_meta[4];           // j, n, kind, done
+  __shared__ int s_meta[4];           // look-back: n, ready, failed, done
   __shared__ uint32_t s_tk[2];
   // LDSIO: raw [3][TC][CT] bf16, later the per-wave store staging (W x 4 planes x 4 rows x CT fp32)
   static_assert(!LDSIO || (K == 1 && L % 8 == 0 && sizeof(RawT) == 2),
                 "LDS-staged I/O: bf16 raw, one channel per lane, rows in eights");
   static_assert(!LDSIO || W * 16 * CT * 4 <= 3 * TC * CT * 2, "store staging exceeds the raw region");
+  static_assert(!LDSIO || kWin * 3 * CT * 4 <= 3 * TC * CT * 2, "look-back staging exceeds the raw region");
   __shared__ __align__(16) bf16_bits s_io[LDSIO ? 3 * TC * CT : 8];
+  // look-back staging of predecessor summaries (LDSIO: the raw region, free after the summary
+  // barrier until the stores)
+  __shared__ float s_pred_own[LDSIO ? 1 : kWin * 3 * CT];
+  float* const s_pred = LDSIO ? reinterpret_cast<float*>(s_io) : s_pred_own;
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -1131,8 +1115,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     ci[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
   }
   if (chunk > 0)
-    lookback_carry<K, W>(chunk, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi, ok, lane,
-                         wave, hdr, s_part, s_carry, s_meta, cr, ci);
+    lookback_carry<K, W, kWin>(chunk, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi, ok,
+                               lane, wave, hdr, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1272,9 +1256,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 // and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
 // then the waves in order) into per-tile partials that fl_param_grad_{segment,final}_kernel add up over
 // the tiles of each channel in a fixed order (deterministic).
-// PF (K = 1, every channel tile full, 16-byte aligned raw rows): the second pass's inputs (z_r,
-// z_i and s_{t-1}) are staged in LDS by 16-byte buffer loads that write LDS directly, issued
-// with the first pass's loads, so that no load latency follows the look-back.
+// The second pass needs s_{t-1} at every step, which the reference reads back from the forward's
+// read (canon:841-850); here each wave recomputes it with the forward recurrence from the state
+// entering its first row (the read at the row before, state_in or 0 at the sequence start),
+// which takes 8 of the 36 bytes per channel and step off the backward's traffic.
+// PF (K = 1, every channel tile full, 16-byte aligned raw rows): the second pass's z_r, z_i are
+// staged in LDS by 16-byte buffer loads that write LDS directly, issued with the first pass's
+// loads, so that no load latency follows the look-back.
 // ------------------------------------------------------------------------------------------
 template <typename RawT, typename GradT, int K, int L, int W, int OCC, bool PF = false>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
@@ -1290,14 +1278,18 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
   __shared__ float s_sum[W][3][CT];   // wave maps (P, Qr, Qi)
-  __shared__ float s_part[W][4][CT];  // look-back partial maps; then parameter-gradient partials
+  __shared__ float s_part[W][4][CT];  // parameter-gradient partials
   __shared__ float s_carry[2][CT];
   __shared__ int s_meta[4];
   __shared__ uint32_t s_tk[2];
-  // PF: z_r, z_i [TC][CT] (RawT), then Re s_{t-1}, Im s_{t-1} [TC][CT] (fp32)
+  // look-back staging of predecessor summaries (a narrower window keeps fp32 raw staging at two
+  // blocks per CU)
+  constexpr int kWin = (PF && sizeof(RawT) == 4) ? lookback_window(K, W) / 2 : lookback_window(K, W);
+  __shared__ float s_pred[kWin * 3 * CT];
+  // PF: z_r, z_i [TC][CT] (RawT)
   constexpr int kPfRaw = TC * CT * (int)sizeof(RawT);
   static_assert(!PF || (K == 1 && L % 8 == 0), "LDS staging: one channel per lane, rows in eights");
-  __shared__ __align__(16) unsigned char s_pf[PF ? 2 * kPfRaw + 2 * TC * CT * 4 : 16];
+  __shared__ __align__(16) unsigned char s_pf[PF ? 2 * kPfRaw : 16];
 
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
@@ -1366,15 +1358,21 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     for (int k = 0; k < K; ++k)
       gv[j][k] = kVacancyMax * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zv[k] * -kLog2e));
   }
-  // s_{t-1} of the tile's rows comes from the forward's read starting one row earlier (from the
-  // tile's own first row for the first tile, whose row before the sequence start is state_in).
-  // Row and row count forced wave-uniform: a descriptor the compiler takes for divergent costs a
-  // readfirstlane loop around every load through it.
-  const bool first = t_begin == 0;
-  const int prev_row = uniform(first ? t_begin : t_begin - 1);
-  const int prev_rows = uniform(first ? rows : rows + 1);
-  const rsrc_t r_prev = make_rsrc(read + ((int64_t)b * T + prev_row) * 4 * C,
-                                  (uint32_t)((int64_t)prev_rows * 4 * C * 4));
+  // the state entering the wave's first row (loaded now, used after the look-back)
+  float s0r[K], s0i[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    s0r[k] = 0.f;
+    s0i[k] = 0.f;
+    if (ok && n_valid > 0 && w0 > 0) {
+      const float* rp = read + ((int64_t)b * T + w0 - 1) * 4 * C + c0 + k;
+      s0r[k] = rp[0];
+      s0i[k] = rp[C];
+    } else if (ok && w0 == 0 && state_in) {
+      s0r[k] = state_in[(int64_t)b * 2 * C + c0 + k];
+      s0i[k] = state_in[(int64_t)b * 2 * C + C + c0 + k];
+    }
+  }
   if constexpr (PF) {
     // raw planes: a row of CT channels is kRawLanes 16-byte pieces, kRawRows rows per load
     constexpr int kRawLanes = CT * (int)sizeof(RawT) / 16, kRawRows = 64 / kRawLanes;
@@ -1387,21 +1385,6 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         __builtin_amdgcn_raw_ptr_buffer_load_lds(
             r_raw, (__attribute__((address_space(3))) void*)&s_pf[p * kPfRaw + r0 * CT * (int)sizeof(RawT)],
             16, vo_r, r0 * raw_row + p * raw_plane, 0, 0);
-      }
-    // s planes: 4 rows of 64 fp32 per load; row r of the tile reads row r - first of r_prev, and
-    // the first tile's row 0 (before the sequence start) an out-of-range offset (state_in later)
-    const int vo_s = ctile * CT * 4 + (lane & 15) * 16;
-#pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-      for (int i = 0; i < L / 4; ++i) {
-        const int r0 = wave * L + 4 * i;
-        const bool head = first && r0 == 0;
-        const int q = lane >> 4;
-        const int vo = head ? (q == 0 ? 0x7fffffff : vo_s + (q - 1) * grd_row) : vo_s + q * grd_row;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(
-            r_prev, (__attribute__((address_space(3))) void*)&s_pf[2 * kPfRaw + (p * TC + r0) * CT * 4],
-            16, vo, head ? p * f_plane : (r0 - (first ? 1 : 0)) * grd_row + p * f_plane, 0, 0);
       }
   }
   if (in_order && threadIdx.x == 0) s_tk[1] = (uint32_t)(epoch_word >> 32);
@@ -1450,10 +1433,12 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   const uint32_t tile_id = (uint32_t)chain * (uint32_t)n_chunks + (uint32_t)ord;
   uint32_t* st_chain = status + (size_t)chain * n_chunks;
   uint64_t* dt = data + (size_t)tile_id * kPlanes * CT + lane * K;
-  if (wave == 0 && ord > 0 && !last_ord) {  // full tile with a successor: publish its map
-    float TP[K], TBr[K], TBi[K];
+  // map of a full tile (ord > 0; wave 0): published as its summary, and applied to its carry for
+  // its inclusive state the way the look-back of later tiles applies it
+  float TP[K], TBr[K], TBi[K];
 #pragma unroll
-    for (int k = 0; k < K; ++k) { TP[k] = 1.f; TBr[k] = 0.f; TBi[k] = 0.f; }
+  for (int k = 0; k < K; ++k) { TP[k] = 1.f; TBr[k] = 0.f; TBi[k] = 0.f; }
+  if (wave == 0 && ord > 0) {
     for (int u = W - 1; u >= 0; --u) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -1462,6 +1447,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         TP[k] *= s_sum[u][0][x];
       }
     }
+  }
+  if (wave == 0 && ord > 0 && !last_ord) {  // full tile with a successor: publish its map
     if (ok) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
@@ -1481,8 +1468,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     ci[k] = (ok && grad_state_out) ? grad_state_out[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
   }
   if (ord > 0)
-    lookback_carry<K, W>(ord, chain, n_chunks, st_chain, data, tag_agg, tag_incl, cTr, cTi, ok, lane,
-                         wave, hdr, s_part, s_carry, s_meta, cr, ci);
+    lookback_carry<K, W, kWin>(ord, chain, n_chunks, st_chain, data, tag_agg, tag_incl, cTr, cTi, ok,
+                               lane, wave, hdr, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1494,11 +1481,15 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           float sr = cr[k], si = ci[k];
-          for (int u = W - 1; u >= 0; --u) {
-            const int x = lane * K + k;
-            float pr, pi;
-            wave_pow(u, k, pr, pi);
-            apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr, si);
+          if (ord > 0) {
+            apply_map(cTr[k], cTi[k], TP[k], TBr[k], TBi[k], sr, si);
+          } else {  // the end of the sequence (maybe partial): its waves' maps one by one
+            for (int u = W - 1; u >= 0; --u) {
+              const int x = lane * K + k;
+              float pr, pi;
+              wave_pow(u, k, pr, pi);
+              apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], sr, si);
+            }
           }
           put_word(dt + 3 * CT + k, sr, tag_incl);
           put_word(dt + 4 * CT + k, si, tag_incl);
@@ -1529,40 +1520,41 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         apply_map(pr, pi, s_sum[u][0][x], s_sum[u][1][x], s_sum[u][2][x], car[k], cai[k]);
       }
     }
-    // every load of the pass first (z_r, z_i, and s_{t-1} from the forward's read), then the
-    // dependent chain: no step waits on memory. Rows past T read as 0 through the descriptor
-    // bounds; the row before the sequence start reads 0 (out-of-range offset) and is replaced by
-    // state_in.
+    // z_r, z_i of the wave's rows (staged in LDS, or every load issued before the dependent
+    // chain; rows past T read as 0 through the descriptor bound), then the forward recurrence
+    // from the state entering the first row: p = s_{t-1} of every row, and z -> tanh(z) in place
     float zr[L][K], zi[L][K], pr[L][K], pi[L][K];
-    {
-      if constexpr (PF) {
-        __builtin_amdgcn_s_waitcnt(0);  // the wave reads only the rows it staged itself
-        const RawT* szr = reinterpret_cast<const RawT*>(s_pf);
-        const float* sp = reinterpret_cast<const float*>(s_pf + 2 * kPfRaw);
+    if constexpr (PF) {
+      __builtin_amdgcn_s_waitcnt(0);  // the wave reads only the rows it staged itself
+      const RawT* szr = reinterpret_cast<const RawT*>(s_pf);
 #pragma unroll
-        for (int j = 0; j < L; ++j) {
-          const int x = (wave * L + j) * CT + lane;
-          zr[j][0] = raw_value(szr[x]);
-          zi[j][0] = raw_value(szr[TC * CT + x]);
-          pr[j][0] = sp[x];
-          pi[j][0] = sp[TC * CT + x];
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < L; ++j) {
-          RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
-          RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi[j]);
-          const int prow = wave * L + j - (first ? 1 : 0);
-          const int so = prow >= 0 ? prow * grd_row : 0x7fffffff;
-          RawLoad<float, K>::run(r_prev, vo_f, so, pr[j]);
-          RawLoad<float, K>::run(r_prev, vo_f, so == 0x7fffffff ? so : so + f_plane, pi[j]);
-        }
+      for (int j = 0; j < L; ++j) {
+        const int x = (wave * L + j) * CT + lane;
+        zr[j][0] = raw_value(szr[x]);
+        zi[j][0] = raw_value(szr[TC * CT + x]);
       }
-      if (w0 == 0) {
+    } else {
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-          pr[0][k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + c0 + k] : 0.f;
-          pi[0][k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
+      for (int j = 0; j < L; ++j) {
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row, zr[j]);
+        RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + raw_plane, zi[j]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      float sr = s0r[k], si = s0i[k];
+#pragma unroll
+      for (int j = 0; j < L; ++j) {
+        // tanh = 1 - 2 / (1 + e^{2z}), as in the forward gates
+        zr[j][k] = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zr[j][k] * (2.0f * kLog2e))), 1.0f);
+        zi[j][k] = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zi[j][k] * (2.0f * kLog2e))), 1.0f);
+        pr[j][k] = sr;
+        pi[j][k] = si;
+        if (j + 1 < n_valid) {  // s_j, needed as p by row j + 1
+          const float v = gv[j][k], gvv = gm[k] * v;
+          const float mr = lr[k] * sr - li[k] * si, mi = lr[k] * si + li[k] * sr;
+          sr = fmaf(1.f - v, mr, gvv * zr[j][k]);
+          si = fmaf(1.f - v, mi, gvv * zi[j][k]);
         }
       }
     }
@@ -1573,9 +1565,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           const float v = gv[j][k], keep = 1.f - v;
-          // tanh = 1 - 2 / (1 + e^{2z}), as in the forward gates
-          const float injr = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zr[j][k] * (2.0f * kLog2e))), 1.0f);
-          const float inji = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zi[j][k] * (2.0f * kLog2e))), 1.0f);
+          const float injr = zr[j][k], inji = zi[j][k];
           const float Gr = uR[j][k] + car[k], Gi = uI[j][k] + cai[k];
           const float p_r = pr[j][k], p_i = pi[j][k];
           const float mr = lr[k] * p_r - li[k] * p_i;     // lam p
@@ -2303,10 +2293,10 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // ticket order as in the forward launch: block order for short chains, one counter otherwise
   const bool in_order = g.n_chunks <= 64;
   float* pgrad = reinterpret_cast<float*>(ws + lay.pgrad_off);
-  // LDS-staged second-pass inputs: every channel tile full, raw rows and read 16-byte aligned
+  // LDS-staged second-pass raw: every channel tile full, raw rows 16-byte aligned
   const int64_t esz = (int64_t)sizeof(RawT);
   const bool pf = FL_BWD_PREFETCH && C % CT == 0 && aligned(raw, 16) && (st * esz) % 16 == 0 &&
-                  (B == 1 || (sb * esz) % 16 == 0) && aligned(read, 16);
+                  (B == 1 || (sb * esz) % 16 == 0);
 #define FL_BWK(PF)                                                                               \
   fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ, PF><<<g.n_tiles, tl.w * 64, 0, stream>>>( \
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma, \

@@ -115,7 +115,9 @@ int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, i
  * deterministic reduction of the parameter gradients.
  *
  *   raw, strides, tr, ti, gamma, state_in   as given to the forward call
- *   read            [B, T, 4C] fp32, the forward output (its state planes are read)
+ *   read            [B, T, 4C] fp32, the forward output (the state planes at every 8th row
+ *                   are read: the state before each 8-step group, from which s_{t-1} of the
+ *                   group's steps is recomputed; the reference reads it back at every step)
  *   grad_read       [B, T, 4C] fp32 contiguous
  *   grad_state_out  [B, 2C] fp32 planar, or NULL (state_out unused)
  *   grad_raw        [B, T, 3C] contiguous, grad_raw_dtype F32 or BF16 (overwritten)
