@@ -501,6 +501,7 @@ def cpu_decode_reforward(runs: int = 3):
             times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     return {"us_per_token_b1": med * 1e6, "batch": 1, "prefix": 2048, "dtype": "fp32",
+            "config1_block_tokens_per_s": 2048 / med,
             "cores": len(os.sched_getaffinity(0)),
             "sample": f"FieldBlock(1024, ff_hidden 2752) seed 0, x ~ N(0,1) [1,2048,1024]; "
                       f"median of {runs} after 1 warm-up; at B=64 the re-forward is ~64x this"}
@@ -682,6 +683,10 @@ def main() -> int:
             result["cpu_baseline"]["decode_reforward"] = cpu_decode_reforward()
             log("[bench] cpu backward ...")
             result["cpu_baseline"]["backward"] = cpu_backward(args.workload)
+            log("[bench] cpu baseline, config 4 ...")
+            long_ctx = cpu_baseline("scan_b1_t65536_d1024", min_runs=3, budget_s=5.0)
+            result["cpu_baseline"]["long_context_b1_t65536"] = {
+                k: long_ctx[k] for k in ("value", "unit", "cores", "kind", "sample")}
 
     print(json.dumps(result), flush=True)
     return 0
