@@ -114,12 +114,18 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
   return bf16_bits_of(lo) | (bf16_bits_of(hi) << 16);
 }
 
+// Output stores (read, grad_raw) are streamed: written once, never read back by the kernel. The
+// non-temporal hint keeps them from displacing the raw data and the look-back words in the
+// caches (B=1, T=65,536: 150.9 -> 126.3 us; bf16 read and the RMSNorm epilogue at B=8, T=2,048
+// 7 % faster).
+constexpr int kStreamStore = 2;  // buffer store cache policy: nt
+
 template <typename OutT, int K>
 struct ReadStore;
 template <>
 struct ReadStore<float, 1> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
-    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[0]), r, vo, so, kStreamStore);
   }
 };
 template <>
@@ -127,7 +133,7 @@ struct ReadStore<float, 2> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
     u32x2 w;
     w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
-    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, kStreamStore);
   }
 };
 template <>
@@ -136,19 +142,21 @@ struct ReadStore<float, 4> {
     u32x4 w;
     w.x = __float_as_uint(v[0]); w.y = __float_as_uint(v[1]);
     w.z = __float_as_uint(v[2]); w.w = __float_as_uint(v[3]);
-    __builtin_amdgcn_raw_buffer_store_b128(w, r, vo, so, 0);
+    // the whole offset in voffset: a 16-byte store with an SGPR soffset is outside the
+    // compiler's wait states for a VALU write of its data VGPRs right after it
+    __builtin_amdgcn_raw_buffer_store_b128(w, r, vo + so, 0, kStreamStore);
   }
 };
 template <>
 struct ReadStore<bf16_bits, 1> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
-    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)bf16_bits_of(v[0]), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)bf16_bits_of(v[0]), r, vo, so, kStreamStore);
   }
 };
 template <>
 struct ReadStore<bf16_bits, 2> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
-    __builtin_amdgcn_raw_buffer_store_b32(bf16_pair(v[0], v[1]), r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(bf16_pair(v[0], v[1]), r, vo, so, kStreamStore);
   }
 };
 template <>
@@ -156,7 +164,7 @@ struct ReadStore<bf16_bits, 4> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, const float* v) {
     u32x2 w;
     w.x = bf16_pair(v[0], v[1]); w.y = bf16_pair(v[2], v[3]);
-    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, 0);
+    __builtin_amdgcn_raw_buffer_store_b64(w, r, vo, so, kStreamStore);
   }
 };
 
@@ -365,7 +373,7 @@ struct WaveTile {
           q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
           __builtin_amdgcn_raw_buffer_store_b128(
               q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
-              0, 0);
+              0, kStreamStore);
         }
       } else {
         // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
@@ -379,7 +387,7 @@ struct WaveTile {
           q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
           __builtin_amdgcn_raw_buffer_store_b128(
               q, w, so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes,
-              0, 0);
+              0, kStreamStore);
         }
       }
     }
