@@ -16,6 +16,8 @@
 // Raw is read and read is written through buffer instructions whose per-step offset is a
 // wave-uniform scalar (the per-lane VGPR offset is just the channel), so the address math costs
 // no vector instructions, and whose descriptor bounds make rows past T read as 0 and drop stores.
+// For bf16 raw with full channel tiles (the default case) raw and read instead pass through LDS,
+// so that every global access is 16 bytes per lane (LDSIO below).
 //
 // The affine map of one step is s -> a*s + b with a = (1-v)*lam and b = gamma*v*inj (complex).
 // Because lam is constant per channel, the map of n full steps is
@@ -27,7 +29,7 @@
 
 #include "fields_amd.h"
 
-// 1: the backward kernel stages its second pass's inputs in LDS where the layout allows (the
+// 1: the backward kernel stages its second pass's z_r, z_i in LDS where the layout allows (the
 // default); 0 keeps register loads everywhere (a build switch for comparisons)
 #ifndef FL_BWD_PREFETCH
 #define FL_BWD_PREFETCH 1
@@ -1298,7 +1300,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
   __shared__ float s_sum[W][3][CT];   // wave maps (P, Qr, Qi)
-  __shared__ float s_part[W][4][CT];  // parameter-gradient partials
+  __shared__ float s_part[W][3][CT];  // parameter-gradient partials (dlam re, im, dgamma)
   __shared__ float s_carry[2][CT];
   __shared__ int s_meta[4];
   __shared__ uint32_t s_tk[2];
