@@ -331,22 +331,24 @@ struct WaveTile {
   }
 
   // materialize() (NORM: materialize_norm()) through a per-wave LDS region `stage` (4 planes x
-  // 4 rows x 64 floats): each group of 4 rows is written to LDS one channel per lane, read back
+  // R rows x 64 floats): each group of R rows is written to LDS one channel per lane, read back
   // as 16 bytes of output per lane (4 fp32 or 8 bf16 channels of one row-plane) and stored with
   // 16-byte buffer stores. The whole store offset is in voffset, so rows past the descriptor's
   // bound (past T) are dropped by it; the tile's 64 channels must all lie below C.
+  static constexpr int kStageRows = L >= 16 ? 4 : 2;  // R
   template <typename OutT, bool NORM>
   __device__ __forceinline__ void materialize_lds(rsrc_t w, int lane, int so0, int row_bytes,
                                                   int plane_bytes, int ch_bytes0, int n,
                                                   float* stage, const float* lr, const float* li,
                                                   float* sr, float* si, float scale,
                                                   const float (*nw)[K], bool keep) const {
-    static_assert(K == 1 && L % 4 == 0, "LDS-staged stores: one channel per lane, rows in fours");
+    constexpr int R = kStageRows;
+    static_assert(K == 1 && L % R == 0, "LDS-staged stores: one channel per lane, whole groups");
 #pragma unroll
-    for (int g = 0; g < L / 4; ++g) {
+    for (int g = 0; g < L / R; ++g) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 4 * g + r;
+      for (int r = 0; r < R; ++r) {
+        const int j = R * g + r;
         const float mr = lr[0] * sr[0] - li[0] * si[0];
         const float mi = lr[0] * si[0] + li[0] * sr[0];
         float o[4];
@@ -364,7 +366,7 @@ struct WaveTile {
           for (int p = 0; p < 4; ++p) o[p] = (o[p] * sc) * nw[p][0];
         }
 #pragma unroll
-        for (int p = 0; p < 4; ++p) stage[(p * 4 + r) * 64 + lane] = o[p];
+        for (int p = 0; p < 4; ++p) stage[(p * R + r) * 64 + lane] = o[p];
       }
       // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
       // the compiler's wait states for a VALU op overwriting the store's data VGPRs right after
@@ -373,13 +375,13 @@ struct WaveTile {
       if constexpr (sizeof(OutT) == 4) {
         // row-plane rp = 4 * i + lane / 16 of instruction i, channels 4 * (lane % 16) .. + 3
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int rp = 4 * i + (lane >> 4), plane = rp >> 2, row = rp & 3, piece = lane & 15;
+        for (int i = 0; i < R; ++i) {
+          const int rp = 4 * i + (lane >> 4), plane = rp / R, row = rp % R, piece = lane & 15;
           const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
           u32x4 q;
           q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
           q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
-          const int off = so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
+          const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
           if (keep) {
             __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kCacheStore);
           } else {
@@ -389,14 +391,14 @@ struct WaveTile {
       } else {
         // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int rp = 8 * i + (lane >> 3), plane = rp >> 2, row = rp & 3, piece = lane & 7;
+        for (int i = 0; i < R / 2; ++i) {
+          const int rp = 8 * i + (lane >> 3), plane = rp / R, row = rp % R, piece = lane & 7;
           const float4 a = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece);
           const float4 c = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece + 4);
           u32x4 q;
           q.x = bf16_pair(a.x, a.y); q.y = bf16_pair(a.z, a.w);
           q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
-          const int off = so0 + 4 * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
+          const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
           if (keep) {
             __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kCacheStore);
           } else {
@@ -1007,7 +1009,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
-  constexpr int kWin = lookback_window(K, W);
+  // LDSIO stages the look-back's summaries in the raw region (3 x TC x CT bf16)
+  constexpr int kWin = LDSIO && TC / 2 < lookback_window(K, W) ? TC / 2 : lookback_window(K, W);
   __shared__ float s_sum[W][3][CT];   // wave summaries (P, Br, Bi)
   __shared__ float s_carry[2][CT];
   __shared__ int s_meta[4];           // look-back: n, ready, failed, done
@@ -1015,7 +1018,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   // LDSIO: raw [3][TC][CT] bf16, later the per-wave store staging (W x 4 planes x 4 rows x CT fp32)
   static_assert(!LDSIO || (K == 1 && L % 8 == 0 && sizeof(RawT) == 2),
                 "LDS-staged I/O: bf16 raw, one channel per lane, rows in eights");
-  static_assert(!LDSIO || W * 16 * CT * 4 <= 3 * TC * CT * 2, "store staging exceeds the raw region");
+  constexpr int kStage = 4 * WaveTile<RawT, K, L>::kStageRows * CT;  // floats of a wave's store stage
+  static_assert(!LDSIO || W * kStage * 4 <= 3 * TC * CT * 2, "store staging exceeds the raw region");
   static_assert(!LDSIO || kWin * 3 * CT * 4 <= 3 * TC * CT * 2, "look-back staging exceeds the raw region");
   __shared__ __align__(16) bf16_bits s_io[LDSIO ? 3 * TC * CT : 8];
   // look-back staging of predecessor summaries (LDSIO: the raw region, free after the summary
@@ -1065,8 +1069,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     // this wave's rows: 8 rows of one plane per instruction (lane = 8 * row + 16-byte piece)
     const int vo = ctile * CT * (int)sizeof(RawT) + (lane >> 3) * io.raw_row + (lane & 7) * 16;
 #pragma unroll
-    for (int q = 0; q < 6; ++q) {
-      const int plane = q >> 1, r0 = wave * L + (q & 1) * 8;
+    for (int q = 0; q < 3 * (L / 8); ++q) {
+      const int plane = q / (L / 8), r0 = wave * L + (q % (L / 8)) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           io.raw, (__attribute__((address_space(3))) void*)&s_io[(plane * TC + r0) * CT], 16, vo,
           r0 * io.raw_row + plane * io.raw_plane, 0, 0);
@@ -1222,7 +1226,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       if (__ballot(sib_failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
       const float scale = rsqrtf(fmaf(tot, inv_n, eps));
       if constexpr (LDSIO) {
-        float* stage = reinterpret_cast<float*>(s_io) + wave * 16 * CT;
+        float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
         tile.template materialize_lds<OutT, true>(io.read, lane, wave * L * io.read_row, io.read_row,
                                                   io.read_plane, ctile * CT * (int)sizeof(OutT),
                                                   n_valid, stage, lr, li, sr, si, scale, nw, keep_out);
@@ -1232,7 +1236,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
                                              si, scale, nw);
       }
     } else if constexpr (LDSIO) {
-      float* stage = reinterpret_cast<float*>(s_io) + wave * 16 * CT;
+      float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
       tile.template materialize_lds<OutT, false>(io.read, lane, wave * L * io.read_row, io.read_row,
                                                  io.read_plane, ctile * CT * (int)sizeof(OutT),
                                                  n_valid, stage, lr, li, sr, si, 0.f, nullptr, keep_out);
