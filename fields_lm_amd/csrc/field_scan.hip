@@ -278,10 +278,21 @@ __device__ __forceinline__ void cpow(float lr, float li, int n, float& pr, float
 }
 
 // s <- A s + B with A = lamn * P (lamn complex, P real)
+// Complex product with its rounding written out (real = fma(ar, br, -(ai bi)), imag =
+// fma(ar, bi, ai br)): left to -ffp-contract=fast, the contraction of such expressions can differ
+// between template instances of one kernel, so their results would not match bit for bit.
+__device__ __forceinline__ void cmul(float ar, float ai, float br, float bi, float& re, float& im) {
+  re = fmaf(ar, br, -(ai * bi));
+  im = fmaf(ar, bi, ai * br);
+}
+
+// s <- P * (lam^n s) + B: applies a summary (P, B) of n steps to the state s. The look-back's
+// carry equals a predecessor's published inclusive state bit for bit only because both are formed
+// by this function with this rounding (cmul, then fma), at whichever call site.
 __device__ __forceinline__ void apply_map(float lnr, float lni, float P, float Br, float Bi,
                                           float& sr, float& si) {
-  const float mr = lnr * sr - lni * si;
-  const float mi = lnr * si + lni * sr;
+  float mr, mi;
+  cmul(lnr, lni, sr, si, mr, mi);
   sr = fmaf(P, mr, Br);
   si = fmaf(P, mi, Bi);
 }
@@ -1399,7 +1410,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
       s0i[k] = state_in[(int64_t)b * 2 * C + C + c0 + k];
     }
   }
-  if constexpr (PF) {
+  // Only a wave with valid rows stages them: it waits for its loads before its second pass
+  // reads them. A wave past T issues none, since one still in flight when the block retires
+  // would write into LDS that a later block on the CU then owns.
+  if (PF && n_valid > 0) {
     // raw planes: a row of CT channels is kRawLanes 16-byte pieces, kRawRows rows per load
     constexpr int kRawLanes = CT * (int)sizeof(RawT) / 16, kRawRows = 64 / kRawLanes;
     const int vo_r = ctile * CT * (int)sizeof(RawT) + (lane / kRawLanes) * raw_row + (lane % kRawLanes) * 16;
@@ -1427,8 +1441,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
           const float keep = 1.f - gv[j][k];
           const float xr = fmaf(keep, Qr[k] + uR[j][k], gv[j][k] * dR[j][k]);
           const float xi = fmaf(keep, Qi[k] + uI[j][k], gv[j][k] * dI[j][k]);
-          Qr[k] = clr[k] * xr - cli[k] * xi;
-          Qi[k] = clr[k] * xi + cli[k] * xr;
+          cmul(clr[k], cli[k], xr, xi, Qr[k], Qi[k]);
           P[k] *= keep;
         }
       }
@@ -1578,7 +1591,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         pi[j][k] = si;
         if (j + 1 < n_valid) {  // s_j, needed as p by row j + 1
           const float v = gv[j][k], gvv = gm[k] * v;
-          const float mr = lr[k] * sr - li[k] * si, mi = lr[k] * si + li[k] * sr;
+          float mr, mi;
+          cmul(lr[k], li[k], sr, si, mr, mi);
           sr = fmaf(1.f - v, mr, gvv * zr[j][k]);
           si = fmaf(1.f - v, mi, gvv * zi[j][k]);
         }
@@ -1592,23 +1606,26 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         for (int k = 0; k < K; ++k) {
           const float v = gv[j][k], keep = 1.f - v;
           const float injr = zr[j][k], inji = zi[j][k];
+          // every product and sum written as explicit fmas (see cmul)
           const float Gr = uR[j][k] + car[k], Gi = uI[j][k] + cai[k];
           const float p_r = pr[j][k], p_i = pi[j][k];
-          const float mr = lr[k] * p_r - li[k] * p_i;     // lam p
-          const float mi = lr[k] * p_i + li[k] * p_r;
-          const float cb = injr * Gr + inji * Gi;         // Re(conj(G) inj)
-          const float dv = (dR[j][k] * mr + dI[j][k] * mi) - (Gr * mr + Gi * mi) + gm[k] * cb;
-          gtr[k] += keep * (Gr * p_r + Gi * p_i) + v * (dR[j][k] * p_r + dI[j][k] * p_i);
-          gti[k] += keep * (Gi * p_r - Gr * p_i) + v * (dI[j][k] * p_r - dR[j][k] * p_i);
-          ggm[k] += v * cb;
+          float mr, mi;  // lam p
+          cmul(lr[k], li[k], p_r, p_i, mr, mi);
+          const float cb = fmaf(injr, Gr, inji * Gi);      // Re(conj(G) inj)
+          const float dDm = fmaf(dR[j][k], mr, dI[j][k] * mi), dGm = fmaf(Gr, mr, Gi * mi);
+          const float dv = fmaf(gm[k], cb, dDm - dGm);
+          const float gp_r = fmaf(Gr, p_r, Gi * p_i), gp_i = fmaf(Gi, p_r, -(Gr * p_i));
+          const float dp_r = fmaf(dR[j][k], p_r, dI[j][k] * p_i), dp_i = fmaf(dI[j][k], p_r, -(dR[j][k] * p_i));
+          gtr[k] = fmaf(keep, gp_r, fmaf(v, dp_r, gtr[k]));
+          gti[k] = fmaf(keep, gp_i, fmaf(v, dp_i, gti[k]));
+          ggm[k] = fmaf(v, cb, ggm[k]);
           const float gvv = gm[k] * v;
-          ozr[k] = gvv * Gr * (1.0f - injr * injr);
-          ozi[k] = gvv * Gi * (1.0f - inji * inji);
-          ozv[k] = dv * v * (1.0f - v * (1.0f / kVacancyMax));
+          ozr[k] = (gvv * Gr) * fmaf(-injr, injr, 1.0f);
+          ozi[k] = (gvv * Gi) * fmaf(-inji, inji, 1.0f);
+          ozv[k] = (dv * v) * fmaf(-v, 1.0f / kVacancyMax, 1.0f);
           const float xr = fmaf(keep, Gr, v * dR[j][k]);
           const float xi = fmaf(keep, Gi, v * dI[j][k]);
-          car[k] = clr[k] * xr - cli[k] * xi;
-          cai[k] = clr[k] * xi + cli[k] * xr;
+          cmul(clr[k], cli[k], xr, xi, car[k], cai[k]);
         }
         if (ok) {  // lanes past C would land in the next plane of the row
           const int so = (wave * L + j) * out_row;

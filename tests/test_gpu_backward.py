@@ -257,11 +257,16 @@ def test_backward_workspace_reuse_across_shapes(dev):
         read = field_scan(raw, tr, ti, gamma)
         gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
         cases.append((raw, tr, ti, gamma, read, gread))
+    from fields_lm_amd import _native as nat
+
     first = [None] * len(cases)
     for rep in range(3):
         for i in ([0, 1, 2, 3] if rep % 2 == 0 else [3, 1, 0, 2]):
             raw, tr, ti, gamma, read, gread = cases[i]
             got = [x.clone() for x in field_scan_backward(raw, tr, ti, gamma, read, gread)[1:]]
+            torch.cuda.synchronize()
+            ws = nat.scan_workspace(dev, 0, "backward")
+            assert nat.workspace_error(ws) == 0, (rep, i)
             if first[i] is None:
                 first[i] = got
                 _, e_tr, e_ti, e_gm, _ = _oracle_grads(raw.cpu(), tr.cpu(), ti.cpu(), gamma.cpu(), gread.cpu())
@@ -269,4 +274,4 @@ def test_backward_workspace_reuse_across_shapes(dev):
                     assert oracle.rel_err(a.cpu(), e) <= TOL, i
             else:
                 for a, b in zip(got, first[i]):
-                    torch.testing.assert_close(a, b, rtol=0, atol=0)
+                    torch.testing.assert_close(a, b, rtol=0, atol=0, msg=lambda m, rep=rep, i=i: f"rep {rep} case {i}: {m}")

@@ -122,7 +122,8 @@ def test_lds_staged_io_equals_register_io(dev):
                 assert oracle.rel_err(a.cpu(), exp_read) <= TOL, (B, T, C)
 
 
-def test_lookback_results_do_not_depend_on_timing(dev):
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32], ids=["bf16", "f32"])
+def test_lookback_results_do_not_depend_on_timing(dev, dtype):
     """The look-back applies the summaries after the nearest published inclusive state one by one,
     as each tile forms its own inclusive state, so the carry is the same float values whichever
     inclusive state a tile found: repeated launches (with other work between them to shift the
@@ -132,14 +133,14 @@ def test_lookback_results_do_not_depend_on_timing(dev):
     from fields_lm_amd import field_scan, field_scan_backward, field_scan_norm
 
     for (B, T, C) in [(16, 1000, 512), (2, 9000, 64), (1, 40000, 128), (8, 2048, 512)]:
-        print(f"[case] determinism B={B} T={T} C={C}", flush=True)
+        print(f"[case] determinism B={B} T={T} C={C} {dtype}", flush=True)
         g = torch.Generator().manual_seed(B + T + C)
-        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype).to(dev)
         tr, ti, gamma = _to(dev, *_params(C, seed=C))
         w = (1.0 + 0.5 * torch.randn(4 * C, generator=g)).to(dev)
         gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
         first = None
-        for rep in range(4):
+        for rep in range(12):
             if rep % 2:  # other launches in between change which tiles run together
                 field_scan(raw[:, : T // 3], tr, ti, gamma)
             read = field_scan(raw, tr, ti, gamma)
