@@ -242,6 +242,34 @@ def test_backward_lds_staged_equals_register_loads(dev, dtype):
         assert oracle.rel_err(a[0].float().cpu(), e_raw) <= tol_raw
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
+def test_backward_repeated_calls_with_empty_waves(dev, dtype):
+    """Regression: T = 1000 leaves the last 64-step tile 40 rows, so three of its eight waves hold
+    no rows. Such a wave once issued its LDS-staged loads without waiting for them, and writes
+    still in flight when the block retired landed in the LDS of the next block on the CU (a few
+    calls in a hundred came out different). 40 calls must give identical gradients."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    B, T, C = 16, 1000, 512
+    print(f"[case] backward repeated calls B={B} T={T} C={C} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(63)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, 63))
+    read = field_scan(raw, tr, ti, gamma)
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    first = None
+    for call in range(40):
+        got = [x.clone() for x in field_scan_backward(raw, tr, ti, gamma, read, gread)]
+        if first is None:
+            first = got
+            continue
+        for a, b in zip(got, first):
+            assert torch.equal(a, b), call
+    torch.cuda.synchronize()
+    assert nat.workspace_error(nat.scan_workspace(dev, 0, "backward")) == 0
+
+
 def test_backward_workspace_reuse_across_shapes(dev):
     """One backward workspace (the per-stream cache), calls alternating shape: the parameter
     gradients of every call equal those of the shape's first call bit for bit (the reduction's
