@@ -834,6 +834,7 @@ struct LookbackHeader {
 constexpr uint32_t kTagAgg = 1u;
 constexpr uint32_t kTagIncl = 2u;
 constexpr uint32_t kTagSib = 3u;   // per-row partial sum of squares (NORM epilogue)
+constexpr uint32_t kTagPart = 3u;  // backward: parameter-gradient partials and segment totals
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
@@ -1291,8 +1292,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 //   dv  = Re(conj(D) lam p) - Re(conj(G) lam p) + gamma Re(conj(G) inj),  dzv = dv v (1 - v/0.9),
 //   dlam += (1 - v) G conj(p) + v D conj(p),   dgamma += v Re(conj(G) inj),
 // and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
-// then the waves in order) into per-tile partials that fl_param_grad_{segment,final}_kernel add up over
-// the tiles of each channel in a fixed order (deterministic).
+// then the waves in order) into per-tile partials, which the same launch adds up over the tiles of
+// each channel tile in a fixed order (segments of rows, then the segment totals; deterministic).
 // The second pass needs s_{t-1} at every step, which the reference reads back from the forward's
 // read (canon:841-850); here each wave recomputes it with the forward recurrence from the state
 // entering its first row (the read at the row before, state_in or 0 at the sequence start),
@@ -1301,6 +1302,57 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 // staged in LDS by 16-byte buffer loads that write LDS directly, issued with the first pass's
 // loads, so that no load latency follows the look-back.
 // ------------------------------------------------------------------------------------------
+// Rows r0 .. r1-1 of a matrix of tagged words (rows of 3 planes of CT words, `base` at this lane's
+// first word), each word awaited until it carries `tag`: wave w adds rows r0+w, r0+w+W, ... in
+// that order into s_acc[w] (the caller adds the waves in order after a barrier), so the sums do not
+// depend on timing. A wave loads kSumRows of its rows at a time. Lanes past C (`ok` false)
+// neither wait nor add.
+template <int K, int W>
+__device__ __forceinline__ void sum_tagged_rows(uint64_t* base, int r0, int r1, uint32_t tag, bool ok,
+                                                int lane, int wave, LookbackHeader* hdr,
+                                                float (&s_acc)[W][3][64 * K]) {
+  constexpr int CT = 64 * K;
+  float a[3][K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) { a[0][k] = 0.f; a[1][k] = 0.f; a[2][k] = 0.f; }
+  uint32_t spins = 0;
+  bool failed = false;
+  constexpr int kSumRows = 4;
+  for (int r = r0 + wave; ok && r < r1 && !failed; r += kSumRows * W) {
+    uint64_t w[kSumRows][3][K];  // rows r, r + W, ..., loaded together
+#pragma unroll
+    for (int q = 0; q < kSumRows; ++q)
+#pragma unroll
+      for (int p = 0; p < 3; ++p)
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+          w[q][p][k] = r + q * W < r1 ? get_word(base + (size_t)(r + q * W) * 3 * CT + p * CT + k) : 0ull;
+#pragma unroll
+    for (int q = 0; q < kSumRows; ++q) {
+      if (r + q * W < r1 && !failed) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
+          if (!settle_words<3>(base + (size_t)(r + q * W) * 3 * CT + k, CT, tag, ww, spins)) {
+            failed = true;
+            break;
+          }
+          a[0][k] += word_value(ww[0]);
+          a[1][k] += word_value(ww[1]);
+          a[2][k] += word_value(ww[2]);
+        }
+      }
+    }
+  }
+  if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    s_acc[wave][0][lane * K + k] = a[0][k];
+    s_acc[wave][1][lane * K + k] = a[1][k];
+    s_acc[wave][2][lane * K + k] = a[2][k];
+  }
+}
+
 template <typename RawT, typename GradT, int K, int L, int W, int OCC, bool PF = false>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
@@ -1308,8 +1360,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     const float* __restrict__ read, const float* __restrict__ grad_read,
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
-    float* __restrict__ grad_state_in, float* __restrict__ pgrad, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, uint32_t n_chains,
+    float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
+    float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
+    uint64_t* part, uint64_t* segw, int seg_rows, uint32_t n_tiles, uint32_t n_chains,
     bool in_order) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
@@ -1651,16 +1704,62 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     s_part[wave][2][lane * K + k] = ggm[k];
   }
   __syncthreads();
+  // The tiles of a channel tile, in ticket order, are its rows r = ord * B + b. Each publishes
+  // its partials as tagged words (row r of `part`); the last row of each segment of seg_rows rows
+  // adds the segment's rows and publishes the total (row of `segw`); the channel tile's last row
+  // adds the segment totals into grad_tr/ti/gamma. Every wait is on lower tickets, and every sum
+  // runs in a fixed order (sum_tagged_rows, then the waves in order): the gradients do not
+  // depend on timing.
+  const int n_b = (int)(n_chains / (uint32_t)n_ctiles);
+  const int n_rows = n_chunks * n_b;
+  const int row = ord * n_b + b;
+  const int n_seg = (n_rows + seg_rows - 1) / seg_rows;
+  const int seg = row / seg_rows;
+  const int r_end = min((seg + 1) * seg_rows, n_rows);
+  const uint32_t tag_part = ((epoch & 0x3fffffffu) << 2) | kTagPart;
+  uint64_t* pw = part + (size_t)ctile * n_rows * 3 * CT + lane * K;
+  uint64_t* sw = segw + (size_t)ctile * n_seg * 3 * CT + lane * K;
   if (wave == 0 && ok) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       const int x = lane * K + k;
       float a0 = 0.f, a1 = 0.f, a2 = 0.f;
       for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
-      float* pg = pgrad + ((size_t)chain * n_chunks + chunk) * 3 * CT + x;
-      pg[0] = a0;
-      pg[CT] = a1;
-      pg[2 * CT] = a2;
+      put_word(pw + (size_t)row * 3 * CT + k, a0, tag_part);
+      put_word(pw + (size_t)row * 3 * CT + CT + k, a1, tag_part);
+      put_word(pw + (size_t)row * 3 * CT + 2 * CT + k, a2, tag_part);
+    }
+  }
+  if (row == r_end - 1) {  // block-uniform: this tile closes its segment
+    __syncthreads();       // s_part is read; reused for the wave totals
+    sum_tagged_rows<K, W>(pw, seg * seg_rows, r_end, tag_part, ok, lane, wave, hdr, s_part);
+    __syncthreads();
+    if (wave == 0 && ok) {
+#pragma unroll
+      for (int k = 0; k < K; ++k) {
+        const int x = lane * K + k;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+        for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
+        put_word(sw + (size_t)seg * 3 * CT + k, a0, tag_part);
+        put_word(sw + (size_t)seg * 3 * CT + CT + k, a1, tag_part);
+        put_word(sw + (size_t)seg * 3 * CT + 2 * CT + k, a2, tag_part);
+      }
+    }
+    if (row == n_rows - 1) {  // the channel tile's last row: add the segment totals
+      __syncthreads();
+      sum_tagged_rows<K, W>(sw, 0, n_seg, tag_part, ok, lane, wave, hdr, s_part);
+      __syncthreads();
+      if (wave == 0 && ok) {
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+          const int x = lane * K + k;
+          float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+          for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
+          grad_tr[c0 + k] = a0;
+          grad_ti[c0 + k] = a1;
+          grad_gamma[c0 + k] = a2;
+        }
+      }
     }
   }
 
@@ -1672,90 +1771,6 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
       __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-  }
-}
-
-// Sum of the per-tile parameter-gradient partials over the batch rows and chunks of each
-// channel, in two deterministic stages: fl_param_grad_segment_kernel adds the partial rows of
-// one segment of (at least kReduceSegRows) rows for 64 channels (waves over interleaved rows, then
-// the waves in order), fl_param_grad_final_kernel adds the segments of 64 channels (waves over
-// interleaved segments, kFinalBatch loads in flight, then the waves in order) into
-// grad_tr/ti/gamma (overwritten). Many segments keep the whole chip busy when B * n_chunks is
-// large; every sum runs in a fixed order, so the gradients are bit-reproducible.
-constexpr int kReduceWaves = 4;
-constexpr int kReduceSegRows = 16;
-constexpr int kFinalBatch = 8;
-
-__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_segment_kernel(
-    const float* __restrict__ pgrad, int B, int C, int n_chunks, int n_ctiles, int CT, int seg_rows,
-    float* __restrict__ seg) {
-  __shared__ float s_acc[kReduceWaves][3][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int ctile = blockIdx.x / (CT / 64);
-  const int x = (blockIdx.x - ctile * (CT / 64)) * 64 + lane;  // channel within the tile
-  const int c = ctile * CT + x;
-  const int n_rows = B * n_chunks;
-  const int r_begin = blockIdx.y * seg_rows;
-  const int r_end = min(r_begin + seg_rows, n_rows);
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-  if (c < C) {
-#pragma unroll 4
-    for (int r = r_begin + wave; r < r_end; r += kReduceWaves) {
-      const int b = r / n_chunks, k = r - b * n_chunks;
-      const float* row = pgrad + ((size_t)(b * n_ctiles + ctile) * n_chunks + k) * 3 * CT + x;
-      a0 += row[0];
-      a1 += row[CT];
-      a2 += row[2 * CT];
-    }
-  }
-  s_acc[wave][0][lane] = a0;
-  s_acc[wave][1][lane] = a1;
-  s_acc[wave][2][lane] = a2;
-  __syncthreads();
-  if (wave == 0 && c < C) {
-    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
-    for (int w = 0; w < kReduceWaves; ++w) { t0 += s_acc[w][0][lane]; t1 += s_acc[w][1][lane]; t2 += s_acc[w][2][lane]; }
-    float* out = seg + (size_t)blockIdx.y * 3 * C + c;
-    out[0] = t0;
-    out[C] = t1;
-    out[2 * C] = t2;
-  }
-}
-
-__global__ __launch_bounds__(kReduceWaves * 64) void fl_param_grad_final_kernel(
-    const float* __restrict__ seg, int n_seg, int C, float* __restrict__ grad_tr,
-    float* __restrict__ grad_ti, float* __restrict__ grad_gamma) {
-  __shared__ float s_acc[kReduceWaves][3][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = uniform(threadIdx.x >> 6);
-  const int c = blockIdx.x * 64 + lane;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-  if (c < C) {
-    for (int i0 = wave; i0 < n_seg; i0 += kReduceWaves * kFinalBatch) {
-      float v[kFinalBatch][3];
-#pragma unroll
-      for (int q = 0; q < kFinalBatch; ++q) {
-        const int i = i0 + q * kReduceWaves;
-        const float* p = seg + (size_t)i * 3 * C + c;
-        v[q][0] = i < n_seg ? p[0] : 0.f;
-        v[q][1] = i < n_seg ? p[C] : 0.f;
-        v[q][2] = i < n_seg ? p[2 * C] : 0.f;
-      }
-#pragma unroll
-      for (int q = 0; q < kFinalBatch; ++q) { a0 += v[q][0]; a1 += v[q][1]; a2 += v[q][2]; }
-    }
-  }
-  s_acc[wave][0][lane] = a0;
-  s_acc[wave][1][lane] = a1;
-  s_acc[wave][2][lane] = a2;
-  __syncthreads();
-  if (wave == 0 && c < C) {
-    float t0 = 0.f, t1 = 0.f, t2 = 0.f;
-    for (int w = 0; w < kReduceWaves; ++w) { t0 += s_acc[w][0][lane]; t1 += s_acc[w][1][lane]; t2 += s_acc[w][2][lane]; }
-    grad_tr[c] = t0;
-    grad_ti[c] = t1;
-    grad_gamma[c] = t2;
   }
 }
 
@@ -2300,13 +2315,15 @@ size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
 }
 
 // Backward tiling (K channels per lane, L steps per wave, W waves, OCC waves per SIMD) and its
-// workspace: [header 2 KiB][status: tiles x u32][data: tiles x 5 x CT x u64][partials: tiles x 3 x CT x f32]
+// workspace: [header 2 KiB][status: tiles x u32][data: tiles x 5 x CT x u64]
+// [partials: tiles x 3 x CT x u64][segment totals: channel tiles x segments x 3 x CT x u64]
 constexpr LookbackTiling kBwdTiling = {1, 8, 8, 4};
+constexpr int kMinSegRows = 16;
 
 struct BwdLayout {
   LookbackGeom g;
-  int n_seg, seg_rows;  // segments of the reduction (at most 65,535) and rows per segment
-  size_t status_off, data_off, pgrad_off, seg_off, bytes;
+  int n_seg, seg_rows;  // segments of the parameter-gradient reduction and rows per segment
+  size_t status_off, data_off, part_off, seg_off, bytes;
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
@@ -2315,12 +2332,16 @@ BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
   w.g = lookback_geom(B, T, C, CT, kBwdTiling.l * kBwdTiling.w);
   w.status_off = kHeaderBytes;
   w.data_off = w.status_off + (size_t)cdiv((int64_t)w.g.n_tiles * 4, 256) * 256;
-  w.pgrad_off = w.data_off + (size_t)cdiv((int64_t)w.g.n_tiles * kPlanes * CT * 8, 256) * 256;
+  w.part_off = w.data_off + (size_t)cdiv((int64_t)w.g.n_tiles * kPlanes * CT * 8, 256) * 256;
+  // segments of about sqrt(rows) rows: a segment's last tile and the channel tile's last tile
+  // each add about sqrt(rows) rows
   const int64_t n_rows = B * (int64_t)w.g.n_chunks;
-  w.seg_rows = (int)(cdiv(n_rows, kReduceSegRows) <= 65535 ? kReduceSegRows : cdiv(n_rows, 65535));
-  w.n_seg = (int)cdiv(n_rows, w.seg_rows);
-  w.seg_off = w.pgrad_off + (size_t)cdiv((int64_t)w.g.n_tiles * 3 * CT * 4, 256) * 256;
-  w.bytes = w.seg_off + (size_t)w.n_seg * 3 * C * sizeof(float);
+  int64_t seg_rows = kMinSegRows;
+  while (seg_rows * seg_rows < n_rows) ++seg_rows;
+  w.seg_rows = (int)seg_rows;
+  w.n_seg = (int)cdiv(n_rows, seg_rows);
+  w.seg_off = w.part_off + (size_t)cdiv((int64_t)w.g.n_tiles * 3 * CT * 8, 256) * 256;
+  w.bytes = w.seg_off + (size_t)cdiv((int64_t)w.g.n_ctiles * w.n_seg * 3 * CT * 8, 256) * 256;
   return w;
 }
 
@@ -2338,7 +2359,6 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
   // ticket order as in the forward launch: block order for short chains, one counter otherwise
   const bool in_order = g.n_chunks <= 64;
-  float* pgrad = reinterpret_cast<float*>(ws + lay.pgrad_off);
   // LDS-staged second-pass raw: every channel tile full, raw rows 16-byte aligned
   const int64_t esz = (int64_t)sizeof(RawT);
   const bool pf = FL_BWD_PREFETCH && C % CT == 0 && aligned(raw, 16) && (st * esz) % 16 == 0 &&
@@ -2346,25 +2366,17 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
 #define FL_BWK(PF)                                                                               \
   fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ, PF><<<g.n_tiles, tl.w * 64, 0, stream>>>( \
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma, \
-      state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in, pgrad, \
-      reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),  \
-      reinterpret_cast<uint64_t*>(ws + lay.data_off), g.n_tiles, (uint32_t)n_chains, in_order)
+      state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
+      grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
+      reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
+      reinterpret_cast<uint64_t*>(ws + lay.part_off), reinterpret_cast<uint64_t*>(ws + lay.seg_off), \
+      lay.seg_rows, g.n_tiles, (uint32_t)n_chains, in_order)
   if (pf) {
     FL_BWK(true);
   } else {
     FL_BWK(false);
   }
 #undef FL_BWK
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return hip_status(e);
-  float* seg = reinterpret_cast<float*>(ws + lay.seg_off);
-  fl_param_grad_segment_kernel<<<dim3((unsigned)(g.n_ctiles * (CT / 64)), (unsigned)lay.n_seg),
-                                 kReduceWaves * 64, 0, stream>>>(pgrad, (int)B, (int)C, g.n_chunks,
-                                                                 g.n_ctiles, CT, lay.seg_rows, seg);
-  e = hipGetLastError();
-  if (e != hipSuccess) return hip_status(e);
-  fl_param_grad_final_kernel<<<(unsigned)cdiv(C, 64), kReduceWaves * 64, 0, stream>>>(
-      seg, lay.n_seg, (int)C, grad_tr, grad_ti, grad_gamma);
   return hip_status(hipGetLastError());
 }
 

@@ -272,8 +272,9 @@ def test_backward_repeated_calls_with_empty_waves(dev, dtype):
 
 def test_backward_workspace_reuse_across_shapes(dev):
     """One backward workspace (the per-stream cache), calls alternating shape: the parameter
-    gradients of every call equal those of the shape's first call bit for bit (the reduction's
-    per-column counts start at 0 whatever an earlier shape left in the workspace)."""
+    gradients of every call equal those of the shape's first call bit for bit (the in-launch
+    reduction never sums a partial an earlier call or shape left in the workspace: its words carry
+    the launch's epoch)."""
     from fields_lm_amd import field_scan, field_scan_backward
 
     print("[case] backward workspace reuse", flush=True)
