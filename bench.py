@@ -314,7 +314,7 @@ def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
     return {"workload": workload, "us_per_step": ev * 1e3, "tokens_per_s": B * T / (ev * 1e-3),
             "bytes_per_token": nbytes // (B * T), "gbs": nbytes / (ev * 1e-3) / 1e9,
             "frac_hbm_peak": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "note": "includes the parameter-gradient reduction launch"}
+            "note": "one launch: the reverse scan and the parameter-gradient reduction"}
 
 
 def _promoted_model(dev):
