@@ -159,6 +159,32 @@ def test_backward_full_size_config2_row(dev):
     assert oracle.rel_err(g_tr.cpu(), sum(x.double() for x in rows).cpu()) <= 1e-5
 
 
+def test_backward_many_reduction_rows(dev):
+    """B=48, T=1500 (24 chunks, the last partial): 1,152 partial rows per channel tile, reduced in
+    34 segments of up to 34 rows. Batch rows are independent, so the parameter gradients equal the
+    sum of those of four calls on 12 rows each, and grad_raw equals theirs bit for bit (a tile's
+    arithmetic does not depend on B); repeated calls give the same bits."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    print("[case] backward many reduction rows", flush=True)
+    B, T, C = 48, 1500, 128
+    g = torch.Generator().manual_seed(48)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, 48))
+    read = field_scan(raw, tr, ti, gamma)
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    full = field_scan_backward(raw, tr, ti, gamma, read, gread)
+    again = field_scan_backward(raw, tr, ti, gamma, read, gread)
+    parts = [field_scan_backward(raw[i:i + 12], tr, ti, gamma, read[i:i + 12].contiguous(),
+                                 gread[i:i + 12].contiguous()) for i in range(0, B, 12)]
+    torch.cuda.synchronize()
+    assert torch.equal(full[0], torch.cat([p[0] for p in parts]))
+    for j in (1, 2, 3):
+        assert oracle.rel_err(full[j].cpu(), sum(p[j].double() for p in parts).cpu()) <= 1e-5, j
+    for x, y in zip(full, again):
+        assert torch.equal(x, y)
+
+
 def test_fused_field_read_autograd(dev):
     """fused_field_read's backward (autograd) equals the oracle's gradients, through the
     transition parameters' torch graph as well."""
