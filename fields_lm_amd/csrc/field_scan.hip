@@ -1302,55 +1302,68 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 // staged in LDS by 16-byte buffer loads that write LDS directly, issued with the first pass's
 // loads, so that no load latency follows the look-back.
 // ------------------------------------------------------------------------------------------
-// Rows r0 .. r1-1 of a matrix of tagged words (rows of 3 planes of CT words, `base` at this lane's
-// first word), each word awaited until it carries `tag`: wave w adds rows r0+w, r0+w+W, ... in
-// that order into s_acc[w] (the caller adds the waves in order after a barrier), so the sums do not
-// depend on timing. A wave loads kSumRows of its rows at a time. Lanes past C (`ok` false)
-// neither wait nor add.
+// Two sums over rows of tagged-word matrices (rows of 3 planes of CT words, each base at this
+// lane's first word): rows a0 .. a1-1 of A into acc_a and rows b0 .. b1-1 of B into acc_b, each
+// word awaited until it carries `tag`. Wave w adds rows a0+w, a0+w+W, ... of A in that order into
+// acc_a[w], and likewise for B (the caller adds the waves in order after a barrier), so the sums do
+// not depend on timing. A wave loads kSumRows of its rows of both matrices at a time. Lanes past C
+// (`ok` false) neither wait nor add.
 template <int K, int W>
-__device__ __forceinline__ void sum_tagged_rows(uint64_t* base, int r0, int r1, uint32_t tag, bool ok,
-                                                int lane, int wave, LookbackHeader* hdr,
-                                                float (&s_acc)[W][3][64 * K]) {
+__device__ __forceinline__ void sum_tagged_rows(uint64_t* base_a, int a0, int a1, uint64_t* base_b,
+                                                int b0, int b1, uint32_t tag, bool ok, int lane,
+                                                int wave, LookbackHeader* hdr,
+                                                float (&acc_a)[W][3][64 * K],
+                                                float (&acc_b)[W][3][64 * K]) {
   constexpr int CT = 64 * K;
-  float a[3][K];
+  constexpr int kSumRows = 4;
+  float sa[3][K], sb[3][K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) { a[0][k] = 0.f; a[1][k] = 0.f; a[2][k] = 0.f; }
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int k = 0; k < K; ++k) { sa[p][k] = 0.f; sb[p][k] = 0.f; }
   uint32_t spins = 0;
   bool failed = false;
-  constexpr int kSumRows = 4;
-  for (int r = r0 + wave; ok && r < r1 && !failed; r += kSumRows * W) {
-    uint64_t w[kSumRows][3][K];  // rows r, r + W, ..., loaded together
+  // settle rows r of one matrix (loaded as w) and add them in order
+  auto settle_add = [&](uint64_t* base, int r, int r_end, uint64_t (&w)[3][K], float (&acc)[3][K]) {
+    if (r >= r_end || failed) return;
 #pragma unroll
-    for (int q = 0; q < kSumRows; ++q)
+    for (int k = 0; k < K; ++k) {
+      uint64_t ww[3] = {w[0][k], w[1][k], w[2][k]};
+      if (!settle_words<3>(base + (size_t)r * 3 * CT + k, CT, tag, ww, spins)) {
+        failed = true;
+        return;
+      }
+      acc[0][k] += word_value(ww[0]);
+      acc[1][k] += word_value(ww[1]);
+      acc[2][k] += word_value(ww[2]);
+    }
+  };
+  for (int i = wave; ok && !failed && (a0 + i < a1 || b0 + i < b1); i += kSumRows * W) {
+    uint64_t wa[kSumRows][3][K], wb[kSumRows][3][K];  // rows i, i + W, ... of A and B
+#pragma unroll
+    for (int q = 0; q < kSumRows; ++q) {
+      const int ra = a0 + i + q * W, rb = b0 + i + q * W;
 #pragma unroll
       for (int p = 0; p < 3; ++p)
 #pragma unroll
-        for (int k = 0; k < K; ++k)
-          w[q][p][k] = r + q * W < r1 ? get_word(base + (size_t)(r + q * W) * 3 * CT + p * CT + k) : 0ull;
-#pragma unroll
-    for (int q = 0; q < kSumRows; ++q) {
-      if (r + q * W < r1 && !failed) {
-#pragma unroll
         for (int k = 0; k < K; ++k) {
-          uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
-          if (!settle_words<3>(base + (size_t)(r + q * W) * 3 * CT + k, CT, tag, ww, spins)) {
-            failed = true;
-            break;
-          }
-          a[0][k] += word_value(ww[0]);
-          a[1][k] += word_value(ww[1]);
-          a[2][k] += word_value(ww[2]);
+          wa[q][p][k] = ra < a1 ? get_word(base_a + (size_t)ra * 3 * CT + p * CT + k) : 0ull;
+          wb[q][p][k] = rb < b1 ? get_word(base_b + (size_t)rb * 3 * CT + p * CT + k) : 0ull;
         }
-      }
     }
+#pragma unroll
+    for (int q = 0; q < kSumRows; ++q) settle_add(base_a, a0 + i + q * W, a1, wa[q], sa);
+#pragma unroll
+    for (int q = 0; q < kSumRows; ++q) settle_add(base_b, b0 + i + q * W, b1, wb[q], sb);
   }
   if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
 #pragma unroll
-  for (int k = 0; k < K; ++k) {
-    s_acc[wave][0][lane * K + k] = a[0][k];
-    s_acc[wave][1][lane * K + k] = a[1][k];
-    s_acc[wave][2][lane * K + k] = a[2][k];
-  }
+  for (int p = 0; p < 3; ++p)
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+      acc_a[wave][p][lane * K + k] = sa[p][k];
+      acc_b[wave][p][lane * K + k] = sb[p][k];
+    }
 }
 
 template <typename RawT, typename GradT, int K, int L, int W, int OCC, bool PF = false>
@@ -1707,9 +1720,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   // The tiles of a channel tile, in ticket order, are its rows r = ord * B + b. Each publishes
   // its partials as tagged words (row r of `part`); the last row of each segment of seg_rows rows
   // adds the segment's rows and publishes the total (row of `segw`); the channel tile's last row
-  // adds the segment totals into grad_tr/ti/gamma. Every wait is on lower tickets, and every sum
-  // runs in a fixed order (sum_tagged_rows, then the waves in order): the gradients do not
-  // depend on timing.
+  // adds its own segment's rows and the earlier segments' totals into grad_tr/ti/gamma. Every
+  // wait is on lower tickets, and every sum runs in a fixed order (sum_tagged_rows, then the
+  // waves in order): the gradients do not depend on timing.
   const int n_b = (int)(n_chains / (uint32_t)n_ctiles);
   const int n_rows = n_chunks * n_b;
   const int row = ord * n_b + b;
@@ -1731,8 +1744,12 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     }
   }
   if (row == r_end - 1) {  // block-uniform: this tile closes its segment
-    __syncthreads();       // s_part is read; reused for the wave totals
-    sum_tagged_rows<K, W>(pw, seg * seg_rows, r_end, tag_part, ok, lane, wave, hdr, s_part);
+    // the channel tile's last row adds the earlier segments' totals in the same pass and never
+    // publishes its own segment's total
+    const bool last = row == n_rows - 1;
+    __syncthreads();  // s_part is read and the wave maps in s_sum are used: both hold wave sums now
+    sum_tagged_rows<K, W>(pw, seg * seg_rows, r_end, sw, 0, last ? seg : 0, tag_part, ok, lane, wave,
+                          hdr, s_part, s_sum);
     __syncthreads();
     if (wave == 0 && ok) {
 #pragma unroll
@@ -1740,24 +1757,16 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         const int x = lane * K + k;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f;
         for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
-        put_word(sw + (size_t)seg * 3 * CT + k, a0, tag_part);
-        put_word(sw + (size_t)seg * 3 * CT + CT + k, a1, tag_part);
-        put_word(sw + (size_t)seg * 3 * CT + 2 * CT + k, a2, tag_part);
-      }
-    }
-    if (row == n_rows - 1) {  // the channel tile's last row: add the segment totals
-      __syncthreads();
-      sum_tagged_rows<K, W>(sw, 0, n_seg, tag_part, ok, lane, wave, hdr, s_part);
-      __syncthreads();
-      if (wave == 0 && ok) {
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const int x = lane * K + k;
-          float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-          for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
-          grad_tr[c0 + k] = a0;
-          grad_ti[c0 + k] = a1;
-          grad_gamma[c0 + k] = a2;
+        if (!last) {
+          put_word(sw + (size_t)seg * 3 * CT + k, a0, tag_part);
+          put_word(sw + (size_t)seg * 3 * CT + CT + k, a1, tag_part);
+          put_word(sw + (size_t)seg * 3 * CT + 2 * CT + k, a2, tag_part);
+        } else {
+          float e0 = 0.f, e1 = 0.f, e2 = 0.f;  // totals of the segments before this one
+          for (int u = 0; u < W; ++u) { e0 += s_sum[u][0][x]; e1 += s_sum[u][1][x]; e2 += s_sum[u][2][x]; }
+          grad_tr[c0 + k] = e0 + a0;
+          grad_ti[c0 + k] = e1 + a1;
+          grad_gamma[c0 + k] = e2 + a2;
         }
       }
     }
