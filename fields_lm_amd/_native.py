@@ -9,6 +9,7 @@ There is no fallback: if the library is missing, every entry point raises Runtim
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
@@ -132,3 +133,22 @@ def workspace_error(ws: torch.Tensor) -> int:
 
     Header: bytes 0..3 tiles done, 128..131 error bits, 256..263 epoch and ticket counter."""
     return int(ws[128:132].view(torch.int32).item())
+
+
+# FIELDS_AMD_CHECK=1: every scan, RMSNorm-epilogue scan and backward call synchronizes its stream
+# and raises if one of its look-back waits gave up (not usable under HIP graph capture).
+CHECK_WAITS = os.environ.get("FIELDS_AMD_CHECK", "0") not in ("", "0")
+
+
+def check_waits(ws: torch.Tensor, what: str) -> None:
+    """With CHECK_WAITS: raise RuntimeError if the workspace's error word is set (bit 0: a wait
+    gave up after its spin limit, so a tile went on without its carry or its partner tiles'
+    values; bit 1: a ticket beyond the launch's tiles), then clear the word so that later calls
+    are checked afresh."""
+    if not CHECK_WAITS:
+        return
+    err = workspace_error(ws)
+    if err:
+        ws[128:132].zero_()
+        raise RuntimeError(f"{what}: a look-back wait gave up (workspace error word {err:#x}); "
+                           "the results of this call are invalid")

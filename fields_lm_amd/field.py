@@ -111,6 +111,7 @@ def field_scan(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torc
             nat.ptr(sout), nat.ptr(read), _read_code(read.dtype), nat.ptr(ws), ws.numel(), algo,
             nat.stream_handle(raw_.device))
         nat.check(code, "fl_scan_forward")
+        nat.check_waits(ws, "fl_scan_forward")
 
     return _scan_call(raw, transition_r, transition_i, gamma, state_in, return_state, read_dtype,
                       launch)
@@ -143,6 +144,7 @@ def field_scan_norm(raw: torch.Tensor, transition_r: torch.Tensor, transition_i:
             nat.ptr(sout), nat.ptr(w), ctypes.c_float(float(eps)), nat.ptr(out),
             _read_code(out.dtype), nat.ptr(ws), ws.numel(), nat.stream_handle(raw_.device))
         nat.check(code, "fl_scan_norm_forward")
+        nat.check_waits(ws, "fl_scan_norm_forward")
 
     if raw.is_cuda:
         _norm_weight(weight, raw.shape[-1] // 3, raw.device)  # shape check before any launch
@@ -189,6 +191,7 @@ def field_scan_backward(raw: torch.Tensor, transition_r: torch.Tensor, transitio
             nat.ptr(g_tr), nat.ptr(g_ti), nat.ptr(g_gm), nat.ptr(g_sin), nat.ptr(ws), ws.numel(),
             nat.stream_handle(dev))
         nat.check(code, "fl_scan_backward")
+        nat.check_waits(ws, "fl_scan_backward")
     elif g_sin is not None and gso is not None:
         g_sin.copy_(gso)
     out = (grad_raw, g_tr, g_ti, g_gm)
@@ -735,4 +738,5 @@ class ScanPlan:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
         code = self.fn(*self.args, ctypes.c_void_p(s.cuda_stream))
         nat.check(code, self.name)
+        nat.check_waits(self.workspace, self.name)
         return self.read

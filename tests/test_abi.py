@@ -153,3 +153,21 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(nat, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(RuntimeError, match="not built"):
         nat.load()
+
+
+def test_wait_check_raises_on_error_word(monkeypatch):
+    """FIELDS_AMD_CHECK: a set error word in the workspace header raises RuntimeError and is
+    cleared; a clear word passes; with the check off nothing is read."""
+    import torch
+
+    ws = torch.zeros(4096, dtype=torch.uint8)
+    monkeypatch.setattr(nat, "CHECK_WAITS", True)
+    nat.check_waits(ws, "fl_scan_forward")
+    ws[128] = 1
+    with pytest.raises(RuntimeError, match="look-back wait gave up"):
+        nat.check_waits(ws, "fl_scan_forward")
+    assert nat.workspace_error(ws) == 0
+    monkeypatch.setattr(nat, "CHECK_WAITS", False)
+    ws[128] = 1
+    nat.check_waits(ws, "fl_scan_forward")
+    assert nat.workspace_error(ws) == 1

@@ -524,3 +524,21 @@ def test_limits_scan_decode_backward(dev, shape):
     (out * gread.double()).sum().backward()
     assert oracle.rel_err(g_raw.cpu(), r.grad) <= TOL
     assert oracle.rel_err(g_tr.cpu(), p[0].grad) <= TOL
+
+
+def test_wait_check_passes_on_real_calls(dev, monkeypatch):
+    """With the FIELDS_AMD_CHECK wait check on, scans (plain, RMSNorm epilogue; block-order and
+    counter tickets) and the backward report no given-up wait."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan, field_scan_backward, field_scan_norm
+
+    monkeypatch.setattr(nat, "CHECK_WAITS", True)
+    for B, T, C in [(8, 2048, 512), (1, 20000, 128)]:
+        print(f"[case] wait check {(B, T, C)}", flush=True)
+        g = torch.Generator().manual_seed(T)
+        raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+        tr, ti, gamma = _to(dev, *_params(C, seed=T))
+        read = field_scan(raw, tr, ti, gamma)
+        field_scan_norm(raw, tr, ti, gamma, torch.ones(4 * C, device=dev), out_dtype=torch.bfloat16)
+        field_scan_backward(raw, tr, ti, gamma, read, torch.randn(B, T, 4 * C, generator=g).to(dev))
+        torch.cuda.synchronize()
