@@ -54,6 +54,36 @@ def copy_calibration() -> int:
     return 0
 
 
+def device_copy_ceiling(scan_bytes: int, scan_gbs: float) -> dict:
+    """Measured device-to-device copy rate on this box (torch ``copy_`` of contiguous buffers, HIP
+    events over back-to-back copies): one copy moving the scan step's algorithmic bytes (read half,
+    write half; the working set fits the 256 MB Infinity Cache, as the scan's does), and one moving
+    2 GiB (HBM only). Reported beside the scan's own rate."""
+    import torch
+
+    out = {}
+    for key, nbytes, reps in (("same_bytes_as_scan_step", scan_bytes, 100), ("two_gib", 2 << 30, 10)):
+        n = nbytes // 2 // 4
+        x = torch.empty(n, device="cuda").uniform_()
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(reps):
+            y.copy_(x)
+        b.record()
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) / reps * 1e3
+        gbs = 2 * n * 4 / (us * 1e-6) / 1e9
+        out[key] = {"bytes_moved": 2 * n * 4, "us_per_copy": us, "gbs": gbs,
+                    "scan_fraction_of_copy": scan_gbs / gbs}
+        del x, y
+        torch.cuda.empty_cache()
+    return out
+
+
 VARIANTS = {  # name -> (ScanPlan keyword arguments, read bytes per element, profile suffix)
     "read_fp32": ({}, 4, ""),
     "read_bf16": ({"read_dtype": "bf16"}, 2, "_read_bf16"),
@@ -612,6 +642,7 @@ def main() -> int:
         extras = {}
         del plan
         torch.cuda.empty_cache()
+        extras["device_copy"] = device_copy_ceiling(alg_bytes, achieved)
         # fp32 raw on the same shape
         wl32 = make_scan_workload(args.workload, dev, dtype=torch.float32)
         p32 = ScanPlan(wl32.raw, wl32.tr, wl32.ti, wl32.gamma)
