@@ -114,25 +114,95 @@ def measured_traffic(workload: str, variant: str = "read_fp32"):
         return None
 
 
-def time_plan(plan, steps: int, warmup: int):
-    """Returns (wall ms per step, event ms per step). Events sit on the launch stream."""
+INFINITY_CACHE_BYTES = 256 * 2**20
+COLD_SET_BYTES = 1 << 30  # rotated buffer sets add up to at least this: 4x the Infinity Cache
+
+
+def time_plan(plans, steps: int, warmup: int):
+    """Times ``steps`` launches; returns (wall ms per step, event ms per step).
+
+    ``plans`` is one plan or a list of plans over distinct buffer sets, launched in rotation
+    (step i runs plans[i % n]); with sets adding up to more than the 256 MB Infinity Cache,
+    every launch finds its inputs in HBM only (cold). The events sit on the launch stream,
+    inside the synchronize bracket that the wall clock spans."""
     import torch
 
-    stream = torch.cuda.current_stream(plan.device)
-    for _ in range(warmup):
-        plan.run(stream)
+    plans = plans if isinstance(plans, (list, tuple)) else [plans]
+    stream = torch.cuda.current_stream(plans[0].device)
+    for i in range(max(warmup, len(plans))):
+        plans[i % len(plans)].run(stream)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(steps):
-        plan.run(stream)
+    for i in range(steps):
+        plans[i % len(plans)].run(stream)
     end.record(stream)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ev_ms = start.elapsed_time(end) / steps
     return wall_ms, ev_ms
+
+
+def cold_sets(set_bytes: int) -> int:
+    """Number of rotated buffer sets for a cold-cache timing: at least 4, and together at least
+    1 GiB, so that between two launches on one set more than the Infinity Cache has streamed."""
+    return max(4, -(-COLD_SET_BYTES // max(set_bytes, 1)))
+
+
+def scan_plans(wl, n_sets: int, **kw):
+    """``n_sets`` ScanPlans over copies of the workload's raw (each with its own read, state and
+    workspace); the first uses the workload's tensor itself."""
+    from fields_lm_amd import ScanPlan
+
+    raws = [wl.raw] + [wl.raw.clone() for _ in range(n_sets - 1)]
+    return [ScanPlan(r, wl.tr, wl.ti, wl.gamma, **kw) for r in raws]
+
+
+def plan_set_bytes(plan) -> int:
+    return (plan.raw.numel() * plan.raw.element_size() + plan.read.numel() * plan.read.element_size()
+            + plan.ws_bytes)
+
+
+def scan_timing(wl, kw: dict, steps: int, warmup: int) -> dict:
+    """One scan variant on a workload, cold (rotated buffer sets) and hot (one set replayed), with
+    its algorithmic bytes per token (raw read once, the output written once)."""
+    import torch
+
+    plans = scan_plans(wl, 1, **kw)
+    n_sets = cold_sets(plan_set_bytes(plans[0]))
+    plans += scan_plans(wl, n_sets, **kw)[1:]
+    _, cold = time_plan(plans, steps, warmup)
+    _, hot = time_plan(plans[0], steps, warmup)
+    from fields_lm_amd.workloads import scan_bytes_per_token
+
+    bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype, plans[0].read.element_size())
+    nb = bpt * wl.tokens
+    del plans
+    torch.cuda.empty_cache()
+    return {"us_per_step": cold * 1e3, "tokens_per_s": wl.tokens / (cold * 1e-3),
+            "bytes_per_token": bpt, "gbs": nb / (cold * 1e-3) / 1e9,
+            "frac_hbm_peak": nb / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "hot_us_per_step": hot * 1e3, "hot_frac_hbm_peak": nb / (hot * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "cache": f"cold: {n_sets} rotated buffer sets; hot: one set replayed"}
+
+
+def cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo), or the platform's processor string."""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def dtype_name(dtype) -> str:
+    import torch
+
+    return {torch.float32: "fp32", torch.bfloat16: "bf16", torch.float16: "fp16"}.get(dtype, str(dtype))
 
 
 def cpu_baseline(workload_name: str, min_runs: int = 5, budget_s: float = 10.0, max_runs: int = 400):
@@ -166,8 +236,8 @@ def cpu_baseline(workload_name: str, min_runs: int = 5, budget_s: float = 10.0, 
         "sample": (f"{workload_name} (B={raw.shape[0]}, T={raw.shape[1]}, C={wl.channels}) raw upcast to "
                    f"fp32; reference_field_read/hierarchical_scan(block 32) restated op for op in torch "
                    f"complex64; median of {runs} passes ({sum(times):.1f} s of CPU work) after 1 "
-                   f"warm-up; {med:.3f} s per pass; "
-                   f"cpu={platform.processor() or platform.machine()}"),
+                   f"warm-up; {med:.3f} s per pass"),
+        "cpu_model": cpu_model(),
     }
 
 
@@ -318,32 +388,49 @@ def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
     dev = torch.device("cuda:0")
     wl = make_scan_workload(workload, dev)
     B, T, C = wl.raw.shape[0], wl.raw.shape[1], wl.channels
-    read = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma)
-    gread = torch.randn(read.shape, device=dev, generator=torch.Generator(device=dev).manual_seed(4))
-    grad_raw = torch.empty(B, T, 3 * C, device=dev, dtype=torch.bfloat16)
-    gp = [torch.empty(C, device=dev) for _ in range(3)]
     lib = nat.load()
     n = int(lib.fl_scan_backward_workspace_bytes(B, T, C))
-    ws = torch.zeros(n, device=dev, dtype=torch.uint8)
     stream = torch.cuda.current_stream(dev)
-    args = (nat.ptr(wl.raw), nat.FL_DTYPE_BF16, B, T, C, wl.raw.stride(0), wl.raw.stride(1), nat.ptr(wl.tr),
-            nat.ptr(wl.ti), nat.ptr(wl.gamma), None, nat.ptr(read), nat.ptr(gread), None, nat.ptr(grad_raw),
-            nat.FL_DTYPE_BF16, *[nat.ptr(x) for x in gp], None, nat.ptr(ws), n,
-            ctypes.c_void_p(stream.cuda_stream))
+    gen = torch.Generator(device=dev).manual_seed(4)
 
     class _Plan:
         device = dev
 
-        def run(self, s=None):
-            nat.check(lib.fl_scan_backward(*args), "fl_scan_backward")
+        def __init__(self, raw):
+            self.raw = raw
+            self.read = field_scan(raw, wl.tr, wl.ti, wl.gamma)
+            self.gread = torch.randn(self.read.shape, device=dev, generator=gen)
+            self.grad_raw = torch.empty(B, T, 3 * C, device=dev, dtype=torch.bfloat16)
+            self.gp = [torch.empty(C, device=dev) for _ in range(3)]
+            self.ws = torch.zeros(n, device=dev, dtype=torch.uint8)
+            self.args = (nat.ptr(raw), nat.FL_DTYPE_BF16, B, T, C, raw.stride(0), raw.stride(1),
+                         nat.ptr(wl.tr), nat.ptr(wl.ti), nat.ptr(wl.gamma), None, nat.ptr(self.read),
+                         nat.ptr(self.gread), None, nat.ptr(self.grad_raw), nat.FL_DTYPE_BF16,
+                         *[nat.ptr(x) for x in self.gp], None, nat.ptr(self.ws), n,
+                         ctypes.c_void_p(stream.cuda_stream))
 
-    _, ev = time_plan(_Plan(), steps, warmup)
+        def run(self, s=None):
+            nat.check(lib.fl_scan_backward(*self.args), "fl_scan_backward")
+
+        def nbytes(self):
+            return sum(t.numel() * t.element_size() for t in (self.raw, self.read, self.gread,
+                                                              self.grad_raw, self.ws))
+
+    plans = [_Plan(wl.raw)]
+    n_sets = cold_sets(plans[0].nbytes())
+    plans += [_Plan(wl.raw.clone()) for _ in range(n_sets - 1)]
+    _, ev = time_plan(plans, steps, warmup)
+    _, hot = time_plan(plans[0], steps, warmup)
     nbytes = (3 * C * 2 + 4 * C * 4 + 3 * C * 2 + 2 * C * 4 // BWD_WAVE_ROWS) * B * T
-    if nat.workspace_error(ws) != 0:
+    if any(nat.workspace_error(p.ws) != 0 for p in plans):
         raise RuntimeError("backward look-back wait gave up")
+    del plans
+    torch.cuda.empty_cache()
     return {"workload": workload, "us_per_step": ev * 1e3, "tokens_per_s": B * T / (ev * 1e-3),
             "bytes_per_token": nbytes // (B * T), "gbs": nbytes / (ev * 1e-3) / 1e9,
             "frac_hbm_peak": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "hot_us_per_step": hot * 1e3, "hot_frac_hbm_peak": nbytes / (hot * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "cache": f"cold: {n_sets} rotated buffer sets; hot: one set replayed",
             "note": "one launch: the reverse scan and the parameter-gradient reduction"}
 
 
@@ -552,6 +639,9 @@ def main() -> int:
                     help="only the backward scan (fl_scan_backward) on --workload")
     ap.add_argument("--model", choices=["prefill", "decode"],
                     help="only the whole-model run: prefill (config 3) or decode (config 5)")
+    ap.add_argument("--cold-only", action="store_true",
+                    help="time the headline scan cold only (no hot-cache replay): every launch of the "
+                         "process then reads cold buffers, so a kernel trace's average is the cold time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -597,33 +687,44 @@ def main() -> int:
         kw["norm_weight"] = torch.ones(4 * wl.channels, device=dev)  # read_norm's init weight
     if not vkw.get("norm"):
         kw["algo"] = ALGOS[args.algo]
-    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
-    wall_ms, ev_ms = time_plan(plan, args.steps, args.warmup)
-    bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype, read_bytes)
+    # cold: rotated buffer sets, every launch reads its raw from HBM (the headline); hot: one
+    # buffer set replayed, its working set resident in the Infinity Cache (reported beside)
+    probe = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
+    n_sets = cold_sets(plan_set_bytes(probe))
+    del probe
+    plans = scan_plans(wl, n_sets, **kw)
+    wall_ms, ev_ms = time_plan(plans, args.steps, args.warmup)
+    hot_ev_ms = None if args.cold_only else time_plan(plans[0], args.steps, args.warmup)[1]
+    out_dtype = plans[0].read.dtype
+    bpt = scan_bytes_per_token(wl.channels, wl.raw.dtype, out_dtype.itemsize)
     alg_bytes = bpt * wl.tokens
     achieved = alg_bytes / (ev_ms * 1e-3) / 1e9
-    log(f"[bench] {args.workload}: wall {wall_ms * 1e3:.1f} us/step, events {ev_ms * 1e3:.1f} us/step, "
-        f"{achieved:.0f} GB/s")
+    log(f"[bench] {args.workload}: cold {ev_ms * 1e3:.1f} us/step (wall {wall_ms * 1e3:.1f}), "
+        f"{achieved:.0f} GB/s; hot {hot_ev_ms * 1e3 if hot_ev_ms else float('nan'):.1f} us/step")
 
     result = {
         "metric": METRIC,
-        "value": wl.tokens / (wall_ms * 1e-3),
+        "value": wl.tokens / (ev_ms * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": wall_ms,
+        "ms_per_step": ev_ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": dtype_name(torch.float32),  # the recurrence's state and arithmetic
         "data": "synthetic",
         "config": {
             "workload": args.workload, "variant": args.variant, "algo": args.algo,
             "B": wl.raw.shape[0], "T": wl.raw.shape[1], "d_model": 2 * wl.channels,
-            "raw_dtype": "bf16", "read_dtype": "fp32" if read_bytes == 4 else "bf16",
-            "state_dtype": "fp32", "read_norm_fused": bool(vkw.get("norm")),
+            "raw_dtype": dtype_name(wl.raw.dtype), "read_dtype": dtype_name(out_dtype),
+            "state_dtype": dtype_name(plans[0].state_out.dtype), "read_norm_fused": bool(vkw.get("norm")),
             "bytes_per_token": bpt, "parallelism": "single-gpu",
+            "cache": f"cold: {n_sets} rotated buffer sets of {plan_set_bytes(plans[0]) / 1e6:.0f} MB",
+            "clock": "HIP events on the launch stream around the timed steps (value, ms_per_step, "
+                     "achieved); wall_ms_per_step is the host clock around the same steps",
+            "wall_ms_per_step": wall_ms,
         },
         "roofline": {
             "bound": "hbm",
@@ -637,49 +738,46 @@ def main() -> int:
             "event_us_per_launch": ev_ms * 1e3,
         },
     }
+    if hot_ev_ms is not None:
+        result["roofline"]["hot_cache"] = {
+            "event_us_per_launch": hot_ev_ms * 1e3,
+            "achieved": alg_bytes / (hot_ev_ms * 1e-3) / 1e9,
+            "frac": alg_bytes / (hot_ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "note": "one buffer set replayed: its working set stays in the 256 MB Infinity Cache "
+                    "between launches"}
 
     if not args.no_extras:
         extras = {}
-        del plan
+        del plans
         torch.cuda.empty_cache()
         extras["device_copy"] = device_copy_ceiling(alg_bytes, achieved)
         # fp32 raw on the same shape
         wl32 = make_scan_workload(args.workload, dev, dtype=torch.float32)
-        p32 = ScanPlan(wl32.raw, wl32.tr, wl32.ti, wl32.gamma)
-        _, e32 = time_plan(p32, 50, 5)
-        b32 = scan_bytes_per_token(wl32.channels, torch.float32) * wl32.tokens
-        extras["fp32_raw"] = {"us_per_step": e32 * 1e3, "tokens_per_s": wl32.tokens / (e32 * 1e-3),
-                              "gbs": b32 / (e32 * 1e-3) / 1e9}
-        del p32, wl32
+        extras["fp32_raw"] = scan_timing(wl32, {}, 50, 5)
+        del wl32
         torch.cuda.empty_cache()
         # config 4: long context
         wll = make_scan_workload("scan_b1_t65536_d1024", dev)
-        pl = ScanPlan(wll.raw, wll.tr, wll.ti, wll.gamma)
-        _, el = time_plan(pl, 20, 3)
-        bl = scan_bytes_per_token(wll.channels, wll.raw.dtype) * wll.tokens
-        extras["long_context_b1_t65536"] = {"us_per_step": el * 1e3, "tokens_per_s": wll.tokens / (el * 1e-3),
-                                            "gbs": bl / (el * 1e-3) / 1e9,
-                                            "frac_hbm_peak": bl / (el * 1e-3) / 1e9 / HBM_PEAK_GBS}
-        del pl, wll
+        extras["long_context_b1_t65536"] = scan_timing(wll, {}, 20, 3)
+        del wll
         torch.cuda.empty_cache()
         # bf16 read, fused read_norm (bf16 / fp32 out), and the unfused sequence it replaces
         wl = make_scan_workload(args.workload, dev)
         C = wl.channels
         w = torch.ones(4 * C, device=dev)
-        for key, kw, read_bytes in [("bf16_read", dict(read_dtype=torch.bfloat16), 2),
-                                    ("fused_read_norm_bf16_out", dict(read_dtype=torch.bfloat16, norm_weight=w), 2),
-                                    ("fused_read_norm_fp32_out", dict(norm_weight=w), 4)]:
-            pp = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, **kw)
-            _, e = time_plan(pp, 100, 10)
-            nb = scan_bytes_per_token(C, wl.raw.dtype, read_bytes) * wl.tokens
-            extras[key] = {"us_per_step": e * 1e3, "tokens_per_s": wl.tokens / (e * 1e-3),
-                           "bytes_per_token": nb // wl.tokens, "gbs": nb / (e * 1e-3) / 1e9,
-                           "frac_hbm_peak": nb / (e * 1e-3) / 1e9 / HBM_PEAK_GBS}
-            del pp
+        for key, kw in [("bf16_read", dict(read_dtype=torch.bfloat16)),
+                        ("fused_read_norm_bf16_out", dict(read_dtype=torch.bfloat16, norm_weight=w)),
+                        ("fused_read_norm_fp32_out", dict(norm_weight=w))]:
+            extras[key] = scan_timing(wl, kw, 100, 10)
+        wll = make_scan_workload("scan_b1_t65536_d1024", dev)
+        extras["long_context_fused_read_norm_bf16_out"] = scan_timing(
+            wll, dict(read_dtype=torch.bfloat16, norm_weight=torch.ones(4 * wll.channels, device=dev)), 20, 3)
+        del wll
+        torch.cuda.empty_cache()
         from fields_lm_amd import RMSNorm
 
         norm = RMSNorm(4 * C).to(dev)
-        pp = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma)
+        pp = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma)  # hot cache, as the fused variants' hot figure
 
         class _Unfused:
             device = dev

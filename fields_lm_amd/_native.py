@@ -110,6 +110,71 @@ def stream_handle(device: torch.device) -> ctypes.c_void_p:
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
+# Workspace header (the C ABI, include/fields_amd.h): bytes 128..131 the error word, 384..387 the
+# spin limit of the kernels' bounded waits (0: 2^20 polls), 392..399 the address of a host-visible
+# 32-bit word that the kernels also set when they set the error word (0: none).
+ERROR_OFFSET = 128
+SPIN_LIMIT_OFFSET = 384
+HOST_ERROR_OFFSET = 392
+# Published words carry 30 bits of a launch epoch that every launch advances, so a workspace is
+# zero-filled again before 2^30 launches have run on it; the wrappers do it every 2^29 calls.
+REZERO_CALLS = 1 << 29
+
+
+class WorkspaceGuard:
+    """Host side of one workspace: a pinned host word whose address sits in the header (the
+    kernels set it when a bounded wait gives up, so no device read is needed to see it) and the
+    count of calls since the workspace was zero-filled."""
+
+    def __init__(self, ws: torch.Tensor):
+        self.host_error = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.calls = 0
+        self.arm(ws)
+
+    def arm(self, ws: torch.Tensor) -> None:
+        addr = torch.tensor([self.host_error.data_ptr()], dtype=torch.int64).view(torch.uint8)
+        ws[HOST_ERROR_OFFSET:HOST_ERROR_OFFSET + 8].copy_(addr)
+
+    def before_call(self, ws: torch.Tensor, what: str) -> None:
+        """Raise RuntimeError if an earlier call on this workspace had a wait give up (its outputs
+        hold NaN where a value was missing); re-zero the workspace when the epoch is due to wrap."""
+        if int(self.host_error[0]) != 0:
+            self.host_error.zero_()
+            ws[ERROR_OFFSET:ERROR_OFFSET + 4].zero_()
+            raise RuntimeError(
+                f"{what}: an earlier call on this workspace had a look-back wait give up; the "
+                "outputs of that call are invalid (NaN where a carry or a partner value was missing)")
+        self.calls += 1
+        if self.calls >= REZERO_CALLS and not torch.cuda.is_current_stream_capturing():
+            ws.zero_()
+            self.arm(ws)
+            self.calls = 0
+
+
+_guards: dict = {}
+
+
+def guard_workspace(ws: torch.Tensor) -> WorkspaceGuard:
+    """The guard of a zero-filled workspace tensor (created on first use: writes the host word's
+    address into the header)."""
+    key = (ws.device.index, ws.data_ptr())
+    g = _guards.get(key)
+    if g is None:
+        g = WorkspaceGuard(ws)
+        _guards[key] = g
+    return g
+
+
+def before_call(ws: torch.Tensor, what: str) -> None:
+    guard_workspace(ws).before_call(ws, what)
+
+
+def set_spin_limit(ws: torch.Tensor, polls: int) -> None:
+    """Polls a bounded wait of the kernels makes on this workspace before it gives up (0: the
+    default 2^20). A small limit makes waits give up on purpose (tests of the failure path)."""
+    ws[SPIN_LIMIT_OFFSET:SPIN_LIMIT_OFFSET + 4].copy_(torch.tensor([polls], dtype=torch.int32).view(torch.uint8))
+
+
 # Scan workspaces, one per (device, stream): zero-filled when allocated, then reused as is
 # (the library keeps launch counters in the first 2 KiB and re-arms them after every call).
 _workspaces: dict = {}
@@ -123,32 +188,38 @@ def scan_workspace(device: torch.device, nbytes: int, kind: str = "forward") -> 
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _guards.pop((ws.device.index, ws.data_ptr()), None)
         ws = torch.zeros(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
         _workspaces[key] = ws
+        guard_workspace(ws)
     return ws
 
 
 def workspace_error(ws: torch.Tensor) -> int:
-    """Error word of a scan workspace header (0 = every look-back wait completed).
-
-    Header: bytes 0..3 tiles done, 128..131 error bits, 256..263 epoch and ticket counter."""
-    return int(ws[128:132].view(torch.int32).item())
+    """Error word of a scan workspace header (0 = every look-back wait completed); reads device
+    memory, so it waits for the stream's work."""
+    return int(ws[ERROR_OFFSET:ERROR_OFFSET + 4].view(torch.int32).item())
 
 
 # FIELDS_AMD_CHECK=1: every scan, RMSNorm-epilogue scan and backward call synchronizes its stream
-# and raises if one of its look-back waits gave up (not usable under HIP graph capture).
+# and raises if one of its look-back waits gave up (not usable under HIP graph capture). Without
+# it a wait that gave up is reported at the next call on the workspace (before_call).
 CHECK_WAITS = os.environ.get("FIELDS_AMD_CHECK", "0") not in ("", "0")
 
 
 def check_waits(ws: torch.Tensor, what: str) -> None:
     """With CHECK_WAITS: raise RuntimeError if the workspace's error word is set (bit 0: a wait
     gave up after its spin limit, so a tile went on without its carry or its partner tiles'
-    values; bit 1: a ticket beyond the launch's tiles), then clear the word so that later calls
-    are checked afresh."""
+    values; bit 1: a ticket beyond the launch's tiles), then clear the word (and the host word)
+    so that later calls are checked afresh."""
     if not CHECK_WAITS:
         return
     err = workspace_error(ws)
     if err:
-        ws[128:132].zero_()
+        ws[ERROR_OFFSET:ERROR_OFFSET + 4].zero_()
+        g = _guards.get((ws.device.index, ws.data_ptr()))
+        if g is not None:
+            g.host_error.zero_()
         raise RuntimeError(f"{what}: a look-back wait gave up (workspace error word {err:#x}); "
                            "the results of this call are invalid")

@@ -815,20 +815,27 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
 // read with relaxed agent-scope atomics (device-coherent across XCD L2s). A reader checks
 // each word's own tag, so no fences are needed, and the epoch (bumped by the last block of
 // every launch) makes words of earlier launches stale without clearing the workspace.
-// Waits sleep between polls and give up after kSpinLimit polls (error flag set), so every
-// wave terminates.
+// Waits sleep between polls and give up after the header's spin limit (2^20 polls unless set),
+// so every wave terminates. A wait that gives up sets the error word (and the host-visible word,
+// when the header names one) and poisons what depends on it with NaN: the tile's carry (and so
+// its outputs and every later tile of its chain), its RMSNorm scale, or the parameter-gradient
+// sums, so that a result computed without a value it needed cannot pass for a valid one.
 // ------------------------------------------------------------------------------------------
 // Every word sits in its own 128-byte line: the ticket counter is hammered by the blocks' first
 // atomic (long chains), `done` by their last one.
 struct LookbackHeader {
-  unsigned int done;   // tiles finished in this launch
+  unsigned int done;   // tiles finished in this launch (blocks that refused a ticket included)
   unsigned int pad0[31];
-  unsigned int error;  // bit 0: a wait hit kSpinLimit; bit 1: ticket out of range
+  unsigned int error;  // bit 0: a wait gave up; bit 1: ticket out of range
   unsigned int pad1[31];
   // bits 63..32 launch epoch, bits 31..0 tickets taken in this launch (block-order launches
   // only read the epoch)
   unsigned long long ticket;
   unsigned long long pad2[15];
+  unsigned int spin_limit;        // polls before a wait gives up; 0: kSpinLimit (set by the caller)
+  unsigned int pad3;
+  unsigned long long host_error;  // address of a host-visible u32 also set on error; 0: none
+  unsigned long long pad4[14];
 };
 
 constexpr uint32_t kTagAgg = 1u;
@@ -838,6 +845,40 @@ constexpr uint32_t kTagPart = 3u;  // backward: parameter-gradient partials and 
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
+static_assert(offsetof(LookbackHeader, error) == 128 && offsetof(LookbackHeader, ticket) == 256 &&
+                  offsetof(LookbackHeader, spin_limit) == 384 &&
+                  offsetof(LookbackHeader, host_error) == 392,
+              "header offsets are part of the C ABI");
+
+__device__ __forceinline__ uint32_t spin_limit_of(const LookbackHeader* hdr) {
+  const uint32_t l = __hip_atomic_load(&hdr->spin_limit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return l != 0u ? l : kSpinLimit;
+}
+
+// Sets `bits` in the header's error word and, when the header names one, in the host-visible
+// word (a plain store: the host only tests it for non-zero).
+__device__ __forceinline__ void report_error(LookbackHeader* hdr, uint32_t bits) {
+  atomicOr(&hdr->error, bits);
+  const unsigned long long h =
+      __hip_atomic_load(&hdr->host_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (h != 0ull)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(h), bits, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+
+__device__ __forceinline__ float poison() { return __builtin_nanf(""); }
+
+// Called once per block (one thread), after the block's last use of the workspace: the last
+// block of the launch re-arms the counter for the next launch (next epoch). Blocks that refused
+// a ticket count too, so a counter that was out of range is re-armed by the launch that saw it.
+__device__ __forceinline__ void finish_block(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch) {
+  const unsigned int d = atomicAdd(&hdr->done, 1u);
+  if (d == n_tiles - 1) {
+    const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
+    __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
 constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
 // Look-back window: the predecessors whose summaries one round stages in LDS (3 x CT floats
 // each): 8W/K, at most 64 (one status load)
@@ -858,13 +899,13 @@ __device__ __forceinline__ float word_value(uint64_t w) { return __uint_as_float
 // Wait until every word w[i] (loaded from p[i*stride]) carries `tag`; false if the wait gave up.
 template <int N>
 __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t tag, uint64_t* w,
-                                             uint32_t& spins) {
+                                             uint32_t& spins, uint32_t limit) {
   while (true) {
     bool ready = true;
 #pragma unroll
     for (int i = 0; i < N; ++i) ready = ready && word_tag(w[i]) == tag;
     if (ready) return true;
-    if (++spins > kSpinLimit) return false;
+    if (++spins > limit) return false;
     __builtin_amdgcn_s_sleep(1);
 #pragma unroll
     for (int i = 0; i < N; ++i)
@@ -883,15 +924,15 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
 // inclusive state, or one whose nearest non-summary predecessor has published nothing yet, waits
 // and scans again (an inclusive state reaches every tile within kWin of the lowest unfinished
 // one, whose own predecessor is finished). On return wave 0 holds the carry-in in (cr, ci)
-// (unchanged if a wait gave up, with the error bit set). ``ord`` is the tile's position in its
-// chain's processing order; every predecessor is a full tile.
+// (NaN if a wait gave up after ``limit`` polls, with the error bit set). ``ord`` is the tile's
+// position in its chain's processing order; every predecessor is a full tile.
 template <int K, int W, int kWin>
 __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks, const uint32_t* st_chain,
                                                uint64_t* data, uint32_t tag_agg, uint32_t tag_incl,
                                                const float* lTr, const float* lTi, bool ok, int lane,
-                                               int wave, LookbackHeader* hdr, float* s_pred,
-                                               float (&s_carry)[2][64 * K], int (&s_meta)[4],
-                                               float* cr, float* ci) {
+                                               int wave, LookbackHeader* hdr, uint32_t limit,
+                                               float* s_pred, float (&s_carry)[2][64 * K],
+                                               int (&s_meta)[4], float* cr, float* ci) {
   constexpr int CT = 64 * K;
   static_assert(kWin >= 1 && kWin <= 64, "look-back window of one status load");
   uint32_t spins = 0;
@@ -950,7 +991,7 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
 #pragma unroll
             for (int k = 0; k < K; ++k) {
               uint64_t ww[3] = {w[q][0][k], w[q][1][k], w[q][2][k]};
-              if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins)) { failed = true; break; }
+              if (!settle_words<3>(dp + k, CT, tag_agg, ww, spins, limit)) { failed = true; break; }
               sp[k] = word_value(ww[0]);
               sp[CT + k] = word_value(ww[1]);
               sp[2 * CT + k] = word_value(ww[2]);
@@ -963,21 +1004,23 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
 #pragma unroll
         for (int k = 0; k < K; ++k) {
           uint64_t ww[2] = {get_word(dp + 3 * CT + k), get_word(dp + 4 * CT + k)};
-          if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins)) { failed = true; break; }
+          if (!settle_words<2>(dp + 3 * CT + k, CT, tag_incl, ww, spins, limit)) { failed = true; break; }
           s_carry[0][lane * K + k] = word_value(ww[0]);
           s_carry[1][lane * K + k] = word_value(ww[1]);
         }
       }
     }
     if (__ballot(failed) != 0ull && lane == 0) {
-      atomicOr(&hdr->error, 1u);
+      report_error(hdr, 1u);
       s_meta[2] = 1;
     }
     __syncthreads();
     if (wave == 0) {
       int done = 0;
       if (s_meta[2]) {
-        done = 1;  // a wait gave up: the carry stays state_in / 0
+        done = 1;  // a wait gave up: the carry is poisoned
+#pragma unroll
+        for (int k = 0; k < K; ++k) { cr[k] = poison(); ci[k] = poison(); }
       } else if (ready) {
 #pragma unroll
         for (int k = 0; k < K; ++k) {
@@ -992,9 +1035,11 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
         }
         done = 1;
       } else {
-        if (++spins > kSpinLimit) {
+        if (++spins > limit) {
           done = 1;
-          if (lane == 0) atomicOr(&hdr->error, 1u);
+          if (lane == 0) report_error(hdr, 1u);
+#pragma unroll
+          for (int k = 0; k < K; ++k) { cr[k] = poison(); ci[k] = poison(); }
         }
         __builtin_amdgcn_s_sleep(2);
       }
@@ -1058,11 +1103,15 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     __syncthreads();
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
-    if (ticket >= n_tiles) {  // counter not re-armed by an interrupted launch: refuse, terminate
-      if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
+    if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
+      if (threadIdx.x == 0) {
+        report_error(hdr, 2u);
+        finish_block(hdr, n_tiles, s_tk[1]);
+      }
       return;
     }
   }
+  const uint32_t limit = spin_limit_of(hdr);
   const uint32_t n_chains = n_tiles / (uint32_t)n_chunks;
   const int chunk = (int)(ticket / n_chains);
   const int chain = (int)(ticket - (uint32_t)chunk * n_chains);
@@ -1154,7 +1203,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   }
   if (chunk > 0)
     lookback_carry<K, W, kWin>(chunk, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi, ok,
-                               lane, wave, hdr, s_pred, s_carry, s_meta, cr, ci);
+                               lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1224,7 +1273,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
           for (int q = 0; q < kBatch; ++q) {
             const int sq = s0 + q * kStride;
             if (sq < n_ctiles && !sib_failed) {
-              if (!settle_words<1>(sg + (size_t)sq * TC, 0, tag_sib, &w[q], spins)) {
+              if (!settle_words<1>(sg + (size_t)sq * TC, 0, tag_sib, &w[q], spins, limit)) {
                 sib_failed = true;
               } else {
                 tot += word_value(w[q]);
@@ -1235,8 +1284,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       }
 #pragma unroll
       for (int m = L; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
-      if (__ballot(sib_failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
-      const float scale = rsqrtf(fmaf(tot, inv_n, eps));
+      // a row whose total misses a sibling's partial gets a NaN scale: the lanes holding the
+      // row's words (l, l + L, ...) combine their failures as they combine their sums
+      int row_failed = sib_failed ? 1 : 0;
+#pragma unroll
+      for (int m = L; m < 64; m <<= 1) row_failed |= __shfl_xor(row_failed, m);
+      if (__ballot(sib_failed) != 0ull && lane == 0) report_error(hdr, 1u);
+      const float scale = row_failed ? poison() : rsqrtf(fmaf(tot, inv_n, eps));
       if constexpr (LDSIO) {
         float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
         tile.template materialize_lds<OutT, true>(io.read, lane, wave * L * io.read_row, io.read_row,
@@ -1266,14 +1320,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   }
 
   // the last block of the launch re-arms the counter for the next launch (next epoch)
-  if (threadIdx.x == 0) {
-    const unsigned int d = atomicAdd(&hdr->done, 1u);
-    if (d == n_tiles - 1) {
-      const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
-      __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1311,7 +1358,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 template <int K, int W>
 __device__ __forceinline__ void sum_tagged_rows(uint64_t* base_a, int a0, int a1, uint64_t* base_b,
                                                 int b0, int b1, uint32_t tag, bool ok, int lane,
-                                                int wave, LookbackHeader* hdr,
+                                                int wave, LookbackHeader* hdr, uint32_t limit,
                                                 float (&acc_a)[W][3][64 * K],
                                                 float (&acc_b)[W][3][64 * K]) {
   constexpr int CT = 64 * K;
@@ -1329,7 +1376,7 @@ __device__ __forceinline__ void sum_tagged_rows(uint64_t* base_a, int a0, int a1
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       uint64_t ww[3] = {w[0][k], w[1][k], w[2][k]};
-      if (!settle_words<3>(base + (size_t)r * 3 * CT + k, CT, tag, ww, spins)) {
+      if (!settle_words<3>(base + (size_t)r * 3 * CT + k, CT, tag, ww, spins, limit)) {
         failed = true;
         return;
       }
@@ -1356,13 +1403,13 @@ __device__ __forceinline__ void sum_tagged_rows(uint64_t* base_a, int a0, int a1
 #pragma unroll
     for (int q = 0; q < kSumRows; ++q) settle_add(base_b, b0 + i + q * W, b1, wb[q], sb);
   }
-  if (__ballot(failed) != 0ull && lane == 0) atomicOr(&hdr->error, 1u);
+  if (__ballot(failed) != 0ull && lane == 0) report_error(hdr, 1u);
 #pragma unroll
   for (int p = 0; p < 3; ++p)
 #pragma unroll
-    for (int k = 0; k < K; ++k) {
-      acc_a[wave][p][lane * K + k] = sa[p][k];
-      acc_b[wave][p][lane * K + k] = sb[p][k];
+    for (int k = 0; k < K; ++k) {  // a sum that missed a row is poisoned
+      acc_a[wave][p][lane * K + k] = failed ? poison() : sa[p][k];
+      acc_b[wave][p][lane * K + k] = failed ? poison() : sb[p][k];
     }
 }
 
@@ -1411,11 +1458,15 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     __syncthreads();
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
-    if (ticket >= n_tiles) {
-      if (threadIdx.x == 0) atomicOr(&hdr->error, 2u);
+    if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
+      if (threadIdx.x == 0) {
+        report_error(hdr, 2u);
+        finish_block(hdr, n_tiles, s_tk[1]);
+      }
       return;
     }
   }
+  const uint32_t limit = spin_limit_of(hdr);
   const int ord = (int)(ticket / n_chains);
   const int chain = (int)(ticket - (uint32_t)ord * n_chains);
   const int chunk = n_chunks - 1 - ord;
@@ -1574,7 +1625,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   }
   if (ord > 0)
     lookback_carry<K, W, kWin>(ord, chain, n_chunks, st_chain, data, tag_agg, tag_incl, cTr, cTi, ok,
-                               lane, wave, hdr, s_pred, s_carry, s_meta, cr, ci);
+                               lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1749,7 +1800,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const bool last = row == n_rows - 1;
     __syncthreads();  // s_part is read and the wave maps in s_sum are used: both hold wave sums now
     sum_tagged_rows<K, W>(pw, seg * seg_rows, r_end, sw, 0, last ? seg : 0, tag_part, ok, lane, wave,
-                          hdr, s_part, s_sum);
+                          hdr, limit, s_part, s_sum);
     __syncthreads();
     if (wave == 0 && ok) {
 #pragma unroll
@@ -1773,14 +1824,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   }
 
   // the last block of the launch re-arms the counter for the next launch (next epoch)
-  if (threadIdx.x == 0) {
-    const unsigned int d = atomicAdd(&hdr->done, 1u);
-    if (d == n_tiles - 1) {
-      const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
-      __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2222,15 +2266,29 @@ struct NormArgs {
   float eps;
 };
 
+// Where a launch keeps its look-back state: the header, the status words, the tagged data words
+// and (RMSNorm epilogue) the per-row partials.
+struct WsRegions {
+  LookbackHeader* hdr;
+  uint32_t* status;
+  uint64_t* data;
+  uint64_t* sib;
+};
+
+WsRegions regions_of(void* workspace, int64_t B, int64_t T, int64_t C) {
+  const WorkspaceLayout lay = workspace_layout(B, T, C);
+  char* ws = static_cast<char*>(workspace);
+  return {reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
+          reinterpret_cast<uint64_t*>(ws + lay.data_off), reinterpret_cast<uint64_t*>(ws + lay.sib_off)};
+}
+
 template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
-                    float* state_out, void* read, void* workspace, NormArgs norm,
+                    float* state_out, void* read, const WsRegions& rg, NormArgs norm,
                     hipStream_t stream) {
   constexpr int CT = 64 * K;
   const LookbackGeom g = lookback_geom(B, T, C, CT, W * L);
-  const WorkspaceLayout lay = workspace_layout(B, T, C);
-  char* ws = static_cast<char*>(workspace);
   // Ticket order. Short chains (<= 64 chunks): block i takes tile i, no ticket atomic on the
   // critical path (B=8, T=2,048 with the RMSNorm epilogue 41.4 -> 37.0 us: the channel tiles of a
   // token start together, one per XCD). This relies on the dispatcher issuing each XCD's share of
@@ -2245,17 +2303,15 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       B * T * (3 * C * (int64_t)sizeof(RawT) + 4 * C * (int64_t)sizeof(OutT)) <= kInfinityCacheBytes;
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
-      gamma, state_in, state_out, static_cast<OutT*>(read), reinterpret_cast<LookbackHeader*>(ws),
-      reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off),
-      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)),
-      reinterpret_cast<uint64_t*>(ws + lay.sib_off), keep_out);
+      gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
+      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, keep_out);
   return hip_status(hipGetLastError());
 }
 
 template <typename RawT, typename OutT>
 int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T, int64_t C,
                       int64_t sb, int64_t st, const float* tr, const float* ti, const float* gamma,
-                      const float* state_in, float* state_out, void* read, void* ws,
+                      const float* state_in, float* state_out, void* read, const WsRegions& ws,
                       NormArgs norm, hipStream_t s) {
 #define FL_LB(KK, LL, WW, OO)                                                                  \
   if (kk == KK && tl.l == LL && tl.w == WW && tl.occ == OO)                                     \
@@ -2405,7 +2461,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
               int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
               const float* gamma, const float* state_in, float* state_out, void* read,
               int read_dtype, void* workspace, size_t workspace_bytes_given, int algo,
-              NormArgs norm, void* stream) {
+              NormArgs norm, void* stream, const WsRegions* fixed = nullptr) {
   if (raw_dtype != FL_DTYPE_F32 && raw_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   if (read_dtype != FL_DTYPE_F32 && read_dtype != FL_DTYPE_BF16) return FL_ERR_DTYPE;
   const int base_algo = algo & 0xff;
@@ -2425,10 +2481,14 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   if (raw_stride_t * esz > kMaxRowBytes || 4 * C * osz > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
   if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!raw || !tr || !ti || !gamma || !read) return FL_ERR_INVALID_ARGUMENT;
-  const size_t need = workspace_bytes(B, T, C);
-  if (!workspace || workspace_bytes_given < need) return FL_ERR_WORKSPACE;
-  if (!aligned(raw, esz) || !aligned(read, osz) || !aligned(workspace, 256))
-    return FL_ERR_INVALID_ARGUMENT;
+  if (fixed == nullptr) {
+    const size_t need = workspace_bytes(B, T, C);
+    if (!workspace || workspace_bytes_given < need) return FL_ERR_WORKSPACE;
+    if (!aligned(workspace, 256)) return FL_ERR_INVALID_ARGUMENT;
+  } else if (base_algo == FL_ALGO_CHUNKED3 || variant != 0 || norm.weight != nullptr) {
+    return FL_ERR_INVALID_ARGUMENT;  // fixed regions: the default look-back launch only
+  }
+  if (!aligned(raw, esz) || !aligned(read, osz)) return FL_ERR_INVALID_ARGUMENT;
   if ((state_in && !aligned(state_in, 4)) || (state_out && !aligned(state_out, 4)))
     return FL_ERR_INVALID_ARGUMENT;
   if (norm.weight != nullptr) {
@@ -2445,6 +2505,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool raw16 = raw_dtype == FL_DTYPE_BF16, out16 = read_dtype == FL_DTYPE_BF16;
+  const WsRegions rg = fixed != nullptr ? *fixed : regions_of(workspace, B, T, C);
   if (base_algo == FL_ALGO_CHUNKED3) {
     const int64_t n_chunks = cdiv(T, kChunkT);
     float* agg = reinterpret_cast<float*>(static_cast<char*>(workspace) +
@@ -2470,7 +2531,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
 #define FL_LDSIO(O, N)                                                                          \
   return launch_lookback<bf16_bits, O, tl.k, tl.l, tl.w, tl.occ, N, true>(                      \
       raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, state_out, read,        \
-      workspace, norm, s);
+      rg, norm, s);
     if (norm.weight != nullptr) {
       if (out16) { FL_LDSIO(bf16_bits, true) }
       FL_LDSIO(float, true)
@@ -2482,7 +2543,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   const int lb_variant = variant >= kLdsIoVariant ? 0 : variant;
 #define FL_LBD(R, O)                                                                          \
   return dispatch_lookback<R, O>(lb_variant, k, raw, B, T, C, raw_stride_b, raw_stride_t, tr,  \
-                                 ti, gamma, state_in, state_out, read, workspace, norm, s);
+                                 ti, gamma, state_in, state_out, read, rg, norm, s);
   if (raw16 && out16) FL_LBD(bf16_bits, bf16_bits)
   if (raw16) FL_LBD(bf16_bits, float)
   if (out16) FL_LBD(float, bf16_bits)

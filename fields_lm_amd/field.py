@@ -89,6 +89,7 @@ def _scan_call(raw, transition_r, transition_i, gamma, state_in, return_state, o
         return (out, sout) if return_state else out
     ws_bytes = int(lib.fl_scan_workspace_bytes(batch, length, channels))
     workspace = nat.scan_workspace(dev, ws_bytes)
+    nat.before_call(workspace, "field scan")
     launch(lib, (raw, batch, length, channels, tr, ti, gm, sin, sout, out, workspace))
     return (out, sout) if return_state else out
 
@@ -184,6 +185,7 @@ def field_scan_backward(raw: torch.Tensor, transition_r: torch.Tensor, transitio
     if batch and length and channels:
         ws_bytes = int(lib.fl_scan_backward_workspace_bytes(batch, length, channels))
         ws = nat.scan_workspace(dev, ws_bytes, "backward")
+        nat.before_call(ws, "fl_scan_backward")
         code = lib.fl_scan_backward(
             nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
             raw.stride(1), nat.ptr(tr), nat.ptr(ti), nat.ptr(gm), nat.ptr(sin), nat.ptr(read),
@@ -233,7 +235,9 @@ class _FieldNormReadFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, *grad_outputs):
         raise NotImplementedError(
-            "the HIP Field scan is forward-only: its backward (canon:1020-1105) is not implemented")
+            "the fused read_norm scan never writes read, so it has no backward: with gradients "
+            "enabled the modules run fused_field_read (backward fl_scan_backward) and the RMSNorm "
+            "module instead")
 
 
 def fused_field_read(raw: torch.Tensor, transition_r: torch.Tensor, transition_i: torch.Tensor,
@@ -491,9 +495,11 @@ class IndependentVacancyField(nn.Module):
         self.read_norm = RMSNorm(2 * dim)
         self.out_proj = nn.Linear(2 * dim, dim)
         self.gate_proj = nn.Linear(dim, dim)
-        # dtype of what the scan hands to out_proj. "auto": bf16 when raw is bf16 (bf16
-        # autocast, whose out_proj casts its input to bf16 anyway), else fp32; or a fixed
-        # torch dtype. Not a parameter or buffer: state_dict is unchanged.
+        # dtype of what the fused scan hands to out_proj. "auto": bf16 when raw is bf16 (bf16
+        # autocast, whose out_proj casts its input to bf16 anyway), else fp32; or a fixed torch
+        # dtype. The unfused path (and every path that needs a gradient) keeps read in fp32 under
+        # "auto", as the reference does (canon:1168, 1193). Not a parameter or buffer:
+        # state_dict is unchanged.
         self.read_dtype = "auto"
         # True: read_norm runs inside the scan kernel (fl_scan_norm_forward /
         # fl_decode_norm_step) and the fp32 read never reaches memory; False: the scan writes
@@ -567,9 +573,16 @@ class IndependentVacancyField(nn.Module):
         return True
 
     def _read_dtype(self, raw: torch.Tensor) -> torch.dtype:
+        """Output dtype of the fused scan + read_norm."""
         if self.read_dtype == "auto":
             return torch.bfloat16 if raw.dtype == torch.bfloat16 else torch.float32
         return self.read_dtype
+
+    def _unfused_read_dtype(self) -> torch.dtype:
+        """dtype of ``read`` when read_norm runs as a separate module: fp32 under "auto" (the
+        reference's read, canon:1168-1193), so RMSNorm normalises, and its backward
+        differentiates, the fp32 values."""
+        return torch.float32 if self.read_dtype == "auto" else self.read_dtype
 
     def normed_read(self, x: torch.Tensor, raw: Optional[torch.Tensor] = None) -> torch.Tensor:
         """read_norm(read) of the scan of x: what out_proj consumes (``raw`` = write_proj(x) when
@@ -580,7 +593,7 @@ class IndependentVacancyField(nn.Module):
             return _FieldNormReadFunction.apply(raw, tr, ti, gamma, self.read_norm.weight,
                                                 self.read_norm.eps, self._read_dtype(raw))
         read = fused_field_read(raw, tr, ti, gamma, self.triton_block_c, self.triton_chunk_t,
-                                read_dtype=self._read_dtype(raw))
+                                read_dtype=self._unfused_read_dtype())
         return self.read_norm(read)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -595,7 +608,7 @@ class IndependentVacancyField(nn.Module):
             return field_scan_norm(raw, tr, ti, gamma, self.read_norm.weight, self.read_norm.eps,
                                    state_in=state, return_state=True, out_dtype=self._read_dtype(raw))
         read, new_state = field_scan(raw, tr, ti, gamma, state_in=state, return_state=True,
-                                     read_dtype=self._read_dtype(raw))
+                                     read_dtype=self._unfused_read_dtype())
         return self.read_norm(read), new_state
 
     def prefill(self, x: torch.Tensor, state: Optional[torch.Tensor] = None
@@ -718,6 +731,7 @@ class ScanPlan:
         self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
         self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
         self.workspace = torch.zeros(self.ws_bytes, device=dev, dtype=torch.uint8)  # zero-filled once
+        nat.guard_workspace(self.workspace)
         head = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
                 raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
                 nat.ptr(self.state_out))
@@ -736,6 +750,7 @@ class ScanPlan:
 
     def run(self, stream: Optional[torch.cuda.Stream] = None) -> torch.Tensor:
         s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        nat.before_call(self.workspace, self.name)
         code = self.fn(*self.args, ctypes.c_void_p(s.cuda_stream))
         nat.check(code, self.name)
         nat.check_waits(self.workspace, self.name)

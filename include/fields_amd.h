@@ -71,7 +71,19 @@ extern "C" {
  *   workspace  device scratch of at least fl_scan_workspace_bytes(B, T, C) bytes, 256-byte
  *              aligned, ZERO-FILLED before its first use and then reused as is: its first 2 KiB
  *              hold launch counters that every call leaves ready for the next one. Calls on one
- *              workspace must be stream-ordered (one workspace per stream).
+ *              workspace must be stream-ordered (one workspace per stream). Every launch advances
+ *              a 30-bit epoch kept there: zero-fill the workspace again before 2^30 launches.
+ *
+ * Workspace header (first 2 KiB; little-endian words at these byte offsets):
+ *   128  u32  error word: bit 0 a bounded wait gave up, bit 1 a ticket beyond the launch's tiles
+ *             (set by the kernels, never cleared by them)
+ *   384  u32  spin limit: polls before a wait gives up (0 = 2^20); written by the caller
+ *   392  u64  address of a host-visible (pinned, device-mapped) u32 that the kernels set non-zero
+ *             whenever they set the error word, so a caller can see a failure without reading
+ *             device memory; 0 = none; written by the caller
+ * A wait that gives up makes what depends on it NaN (the tile's outputs and every later tile of
+ * its chain, a row's RMSNorm scale, the backward's gradients), so an output computed without a
+ * value it needed cannot pass for a valid one. The same header leads the backward's workspace.
  */
 int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,

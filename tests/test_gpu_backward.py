@@ -236,6 +236,41 @@ def test_field_block_training_gradients(dev):
         assert oracle.rel_err(got[k], p.grad) <= 2e-4, k
 
 
+def test_autocast_training_keeps_read_fp32(dev):
+    """Training under bf16 autocast: the mixer's read reaches read_norm in fp32 and its gradient
+    reaches the scan's backward in fp32 (canon:1168 ``.float()``, RMSNorm on the fp32 read, the
+    cast to bf16 only at out_proj); the gradients equal those of the same computation written out
+    with an explicit fp32 read."""
+    from fields_lm_amd import IndependentVacancyField, fused_field_read
+
+    print("[case] autocast training read dtype", flush=True)
+    torch.manual_seed(31)
+    mixer = IndependentVacancyField(128, "triton", 32, 32, 64).to(dev)
+    x = torch.randn(2, 50, 128, device=dev)
+    w = torch.randn(2, 50, 128, device=dev)
+    seen = []
+    h1 = mixer.read_norm.register_forward_pre_hook(lambda m, i: seen.append(("in", i[0].dtype)))
+    h2 = mixer.read_norm.register_full_backward_hook(lambda m, gi, go: seen.append(("grad", gi[0].dtype)))
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        y = mixer(x)
+    (y.float() * w).sum().backward()
+    h1.remove()
+    h2.remove()
+    assert ("in", torch.float32) in seen and ("grad", torch.float32) in seen, seen
+    got = {k: p.grad.clone() for k, p in mixer.named_parameters()}
+    mixer.zero_grad()
+    with torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+        raw = mixer.write_proj(x).float()
+        tr, ti, gamma = mixer.transition()
+        read = fused_field_read(raw, tr, ti, gamma)
+        assert read.dtype == torch.float32
+        out = mixer.out_proj(mixer.read_norm(read))
+        y2 = x + (out * torch.sigmoid(mixer.gate_proj(x))).to(x.dtype)
+    (y2.float() * w).sum().backward()
+    for k, p in mixer.named_parameters():
+        assert oracle.rel_err(got[k].float().cpu(), p.grad.float().cpu()) <= 1e-5, k
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["f32", "bf16"])
 def test_backward_lds_staged_equals_register_loads(dev, dtype):
     """The second pass's inputs staged in LDS (every channel tile full, 16-byte aligned raw rows)

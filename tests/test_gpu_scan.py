@@ -450,6 +450,36 @@ def test_block_bf16_autocast_matches_reference_golden(dev, golden_dir):
     assert oracle.rel_err(out.float().cpu(), d["block_out"]) <= TOL_BF16_BLOCK
 
 
+def test_block_bf16_autocast_unfused_matches_reference_golden(dev, golden_dir):
+    """read_norm as a separate module (fuse_read_norm False) under bf16 autocast: the scan hands
+    read_norm an fp32 read, as the reference does (canon:1168, 1193), and the block matches the
+    reference's bf16 output at least as closely as the fused path."""
+    block, _ = _golden_block(golden_dir)
+    d = np.load(golden_dir / "selftest_block_bf16.npz")
+    print("[case] block bf16 golden unfused", flush=True)
+    block = block.to(device=dev, dtype=torch.bfloat16)
+    x = torch.from_numpy(d["x"]).to(device=dev, dtype=torch.bfloat16)
+    seen = []
+    h = block.mixer.read_norm.register_forward_pre_hook(lambda m, i: seen.append(i[0].dtype))
+    errs = {}
+    try:
+        for fused in (True, False):
+            block.mixer.fuse_read_norm = fused
+            with torch.no_grad(), torch.autocast(device_type="cuda", dtype=torch.bfloat16):
+                out = block(x)
+                mix = block.mixer(x)
+            errs[fused] = (oracle.rel_err(out.float().cpu(), d["block_out"]),
+                           oracle.rel_err(mix.float().cpu(), d["mixer_out"]))
+    finally:
+        h.remove()
+        block.mixer.fuse_read_norm = True
+    print(f"[case] errors fused {errs[True]} unfused {errs[False]}", flush=True)
+    assert seen and all(t == torch.float32 for t in seen)  # only the unfused calls, on fp32 read
+    for i in range(2):
+        assert errs[False][i] <= TOL_BF16_BLOCK
+        assert errs[False][i] <= errs[True][i] * 1.02 + 1e-6, (errs[False], errs[True])
+
+
 def test_config1_block_rows_match_reference_golden(dev, golden_dir):
     """Config 1: promoted-geometry block, seed 0, fp32, B=1 T=2048 d=1024 — output rows and the
     final complex state against the reference's CPU path."""

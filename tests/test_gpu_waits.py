@@ -1,0 +1,136 @@
+"""GPU: a look-back wait that gives up is visible: its outputs are NaN, every kernel returns, and
+the next call on the workspace raises RuntimeError (the kernels set a host-visible word named in
+the workspace header, so no device read is needed).
+
+The failure is forced from the host, with every kernel still exiting normally: the workspace's
+ticket counter is pre-seeded so that a launch hands out only its last few tickets (the blocks
+with the others refuse and exit), so the tiles that do run wait on predecessors that never
+publish, and the header's spin limit is 16 polls. The launch after it finds the counter re-armed
+(blocks that refused count toward the launch's end) and is correct again.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from oracle import reference_path as ref
+
+pytestmark = pytest.mark.gpu
+
+TICKET_OFFSET = 256
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no ROCm device")
+    from fields_lm_amd import _native
+
+    _native.load()
+    return torch.device("cuda:0")
+
+
+def _params(C, seed):
+    rl, th = ref.init_radius_theta(C)
+    g = torch.Generator().manual_seed(seed)
+    return ref.transition_params(rl + 0.5 * torch.randn(C, generator=g), th + 0.3 * torch.randn(C, generator=g))
+
+
+def _seed_counter(ws, epoch, first_ticket):
+    """Ticket counter word: epoch in the high half, the next ticket to hand out in the low half."""
+    word = torch.tensor([(epoch << 32) | first_ticket], dtype=torch.int64).view(torch.uint8)
+    ws[TICKET_OFFSET:TICKET_OFFSET + 8].copy_(word)
+
+
+# T = 66 chunks of 128 steps: more than 64 chunks per chain, so tickets come from the counter
+CASES = [(1, 66 * 128, 64, "plain"), (1, 66 * 128 - 5, 128, "norm")]
+
+
+@pytest.mark.parametrize("B,T,C,kind", CASES, ids=[c[3] for c in CASES])
+def test_given_up_wait_poisons_outputs_and_raises(dev, B, T, C, kind):
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd import _native as nat
+
+    print(f"[case] forced give-up {kind} B={B} T={T} C={C}", flush=True)
+    g = torch.Generator().manual_seed(T + C)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+    tr, ti, gamma = _params(C, seed=C)
+    weight = torch.rand(4 * C, generator=g) + 0.5
+    kw = {} if kind == "plain" else {"norm_weight": weight.to(dev)}
+    plan = ScanPlan(raw.to(dev), tr.to(dev), ti.to(dev), gamma.to(dev), **kw)
+    n_ctiles = (C + 63) // 64
+    n_chunks = (T + 127) // 128
+    n_tiles = B * n_ctiles * n_chunks
+    ws = plan.workspace
+    sentinel = 7.0
+    plan.read.fill_(sentinel)
+    # only the last chunk's tiles run (one channel tile waits for its chain's predecessors, and
+    # in the norm case also for the partner channel tile of its rows, which never runs)
+    keep = 1 if kind == "norm" else n_ctiles
+    _seed_counter(ws, epoch=5, first_ticket=n_tiles - keep)
+    nat.set_spin_limit(ws, 16)
+    plan.run()
+    torch.cuda.synchronize()  # every kernel returned
+    err = nat.workspace_error(ws)
+    assert err & 1 and err & 2, hex(err)  # a wait gave up; tickets past the launch were refused
+    read = plan.read.cpu()
+    t_last = (n_chunks - 1) * 128
+    ran = read[:, t_last:]
+    if kind == "plain":
+        assert bool(torch.isnan(ran).all())  # the carry was missing: every value is poisoned
+    else:
+        c_tile = slice(64, 128)  # the tile that ran: the second channel tile
+        planes = [ran[..., p * C:(p + 1) * C][..., c_tile] for p in range(4)]
+        assert all(bool(torch.isnan(x).all()) for x in planes)
+    assert bool((read[:, :t_last] == sentinel).all())  # tiles that never ran wrote nothing
+    # reported at the next call on the workspace, without a device read
+    with pytest.raises(RuntimeError, match="wait give up"):
+        plan.run()
+    # the counter was re-armed by the failed launch: the next call is correct again
+    nat.set_spin_limit(ws, 0)
+    out = plan.run()
+    torch.cuda.synchronize()
+    assert nat.workspace_error(ws) == 0
+    exp, _ = oracle.scan_f64(raw.float(), tr, ti, gamma)
+    if kind == "norm":
+        exp = oracle.rms_norm_f64(exp, weight)
+    assert oracle.rel_err(out.cpu(), exp) <= 1e-4
+
+
+def test_given_up_backward_wait_poisons_gradients(dev):
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    B, T, C = 1, 66 * 64, 64  # 66 chunks of 64 steps (the backward's tiles): counter tickets
+    print(f"[case] forced give-up backward B={B} T={T} C={C}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, seed=3))
+    read = field_scan(raw, tr, ti, gamma)
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    field_scan_backward(raw, tr, ti, gamma, read, gread)  # creates the stream's backward workspace
+    torch.cuda.synchronize()
+    ws = nat.scan_workspace(dev, 0, "backward")
+    n_tiles = 66
+    _seed_counter(ws, epoch=9, first_ticket=n_tiles - 3)
+    nat.set_spin_limit(ws, 16)
+    g_raw, g_tr, g_ti, g_gm = field_scan_backward(raw, tr, ti, gamma, read, gread)
+    torch.cuda.synchronize()
+    err = nat.workspace_error(ws)
+    assert err & 1 and err & 2, hex(err)
+    # tickets are taken in reverse time order: the tiles that ran hold the first rows in time
+    # order 63..65 from the end, i.e. rows 0 .. 3*64; their carries were missing
+    assert bool(torch.isnan(g_raw[:, :3 * 64]).all())
+    with pytest.raises(RuntimeError, match="wait give up"):
+        field_scan_backward(raw, tr, ti, gamma, read, gread)
+    nat.set_spin_limit(ws, 0)
+    g_raw2, g_tr2, _, _ = field_scan_backward(raw, tr, ti, gamma, read, gread)
+    torch.cuda.synchronize()
+    assert nat.workspace_error(ws) == 0
+    r = raw.double().cpu().requires_grad_()
+    p = [t.double().cpu().requires_grad_() for t in (tr, ti, gamma)]
+    out, _ = oracle.scan_f64_autograd(r, *p)
+    (out * gread.double().cpu()).sum().backward()
+    assert oracle.rel_err(g_raw2.cpu(), r.grad) <= 1e-4
+    assert oracle.rel_err(g_tr2.cpu(), p[0].grad) <= 1e-4
