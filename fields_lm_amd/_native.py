@@ -26,7 +26,10 @@ FL_OK = 0
 FL_ERR_INVALID_ARGUMENT = 1
 FL_ERR_DTYPE = 2
 FL_ERR_WORKSPACE = 3
+FL_ERR_CAPTURE = 4
 FL_ERR_HIP_BASE = 1000
+FL_STATIC_MAX_TILES = 12288
+FL_STATIC_SCRATCH_BYTES = 31508480
 
 # every extern "C" symbol of include/fields_amd.h, with (restype, argtypes)
 _vp = ctypes.c_void_p
@@ -39,6 +42,8 @@ SIGNATURES = {
     "fl_scan_forward_ex": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                   _vp, _vp, _int, _vp, _sz, _int, _vp]),
     "fl_scan_workspace_bytes": (_sz, [_i64, _i64, _i64]),
+    "fl_scan_forward_static": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
+                                      _vp, _vp, _int, _vp]),
     "fl_scan_norm_forward": (_int, [_vp, _int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp,
                                     _vp, _vp, ctypes.c_float, _vp, _int, _vp, _sz, _vp]),
     "fl_decode_step": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _vp, _int, _vp]),
@@ -89,6 +94,9 @@ def check(code: int, what: str) -> None:
         raise TypeError(f"{what}: unsupported dtype")
     if code == FL_ERR_WORKSPACE:
         raise RuntimeError(f"{what}: workspace missing or too small")
+    if code == FL_ERR_CAPTURE:
+        raise RuntimeError(f"{what}: the first call on a device sets up its static scratch and "
+                           "must not be made under stream capture")
     if code >= FL_ERR_HIP_BASE:
         raise RuntimeError(f"{what}: HIP error {code - FL_ERR_HIP_BASE}")
     raise RuntimeError(f"{what}: error code {code}")

@@ -27,6 +27,8 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <mutex>
+
 #include "fields_amd.h"
 
 // 1: the backward kernel stages its second pass's z_r, z_i in LDS where the layout allows (the
@@ -2553,6 +2555,79 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
 
 }  // namespace
 
+// ------------------------------------------------------------------------------------------
+// No-allocation variant of fl_scan_forward (fl_scan_forward_static): the look-back state lives in
+// a file-scope device array, `scratch`, one copy per GPU for the life of the process, instead of
+// a caller-provided workspace. Layout: [header 2 KiB][status: kStaticMaxTiles x u32]
+// [data: kStaticMaxTiles x 5 planes x 64 channels x u64]. Launches of the default look-back tiling
+// (64-channel x 128-step tiles) use it; every call on a GPU shares that GPU's array, so calls that
+// overlap on one GPU race. Nothing in it has to start at zero per call: every word carries the
+// epoch that each launch advances. It is zero-filled once, at the first call on each device.
+// ------------------------------------------------------------------------------------------
+namespace {
+constexpr uint32_t kStaticMaxTiles = FL_STATIC_MAX_TILES;
+constexpr size_t kStaticStatusOff = kHeaderBytes;
+constexpr size_t kStaticDataOff = kStaticStatusOff + ((size_t)kStaticMaxTiles * 4 + 255) / 256 * 256;
+constexpr size_t kStaticScratchBytes = kStaticDataOff + (size_t)kStaticMaxTiles * kPlanes * 64 * 8;
+static_assert(kStaticScratchBytes == FL_STATIC_SCRATCH_BYTES, "scratch size stated in fields_amd.h");
+static_assert(kStaticScratchBytes % 16 == 0, "zero-filled in 16-byte stores");
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+namespace {
+
+__global__ __launch_bounds__(256) void fl_fill_zero_kernel(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+struct StaticScratch {
+  std::mutex m;
+  char* ptr[kMaxDevices] = {};  // device address of each GPU's `scratch` (null: not set up)
+};
+
+StaticScratch& static_scratch_state() {
+  static StaticScratch st;
+  return st;
+}
+
+// This GPU's copy of `scratch` (the stream's device): at the first call on a device its address
+// is looked up with that device current and it is zero-filled on `stream` (so that first call
+// must not be under stream capture: a captured fill would re-run on every replay).
+int static_scratch(hipStream_t stream, char** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(stream, &dev);
+  if (e != hipSuccess) return hip_status(e);
+  if (dev < 0 || dev >= kMaxDevices) return FL_ERR_INVALID_ARGUMENT;
+  StaticScratch& st = static_scratch_state();
+  std::lock_guard<std::mutex> lock(st.m);
+  if (st.ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if ((e = hipStreamIsCapturing(stream, &cs)) != hipSuccess) return hip_status(e);
+    if (cs != hipStreamCaptureStatusNone) return FL_ERR_CAPTURE;
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return hip_status(e);
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return hip_status(e);
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return hip_status(e);
+    if (p == nullptr) return FL_ERR_HIP_BASE + (int)hipErrorInvalidSymbol;
+    fl_fill_zero_kernel<<<256, 256, 0, stream>>>(static_cast<uint4*>(p), kStaticScratchBytes / 16);
+    if ((e = hipGetLastError()) != hipSuccess) return hip_status(e);
+    st.ptr[dev] = static_cast<char*>(p);
+  }
+  *out = st.ptr[dev];
+  return FL_OK;
+}
+
+}  // namespace
+
 extern "C" {
 
 int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
@@ -2584,6 +2659,25 @@ int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_
   return fl_scan_forward_ex(raw, raw_dtype, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma,
                             state_in, state_out, read, read_dtype, workspace,
                             workspace_bytes_given, FL_ALGO_AUTO, stream);
+}
+
+int fl_scan_forward_static(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                           int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                           const float* ti, const float* gamma, const float* state_in,
+                           float* state_out, void* read, int read_dtype, void* stream) {
+  constexpr LookbackTiling tl = kLookbackTilings[0];
+  if (B > 0 && T > 0 && C > 0 &&
+      B * cdiv(C, 64 * tl.k) * cdiv(T, (int64_t)tl.l * tl.w) > (int64_t)kStaticMaxTiles)
+    return FL_ERR_WORKSPACE;  // beyond what the static scratch holds
+  char* base = nullptr;
+  const int rc = static_scratch(static_cast<hipStream_t>(stream), &base);
+  if (rc != FL_OK) return rc;
+  const WsRegions rg{reinterpret_cast<LookbackHeader*>(base),
+                     reinterpret_cast<uint32_t*>(base + kStaticStatusOff),
+                     reinterpret_cast<uint64_t*>(base + kStaticDataOff), nullptr};
+  return scan_impl(raw, raw_dtype, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in,
+                   state_out, read, read_dtype, nullptr, 0, FL_ALGO_AUTO, NormArgs{nullptr, 0.f},
+                   stream, &rg);
 }
 
 int fl_decode_step(const void* raw_t, int raw_dtype, int64_t B, int64_t C, int64_t raw_stride_b,

@@ -13,7 +13,8 @@
  * All pointers are device pointers unless stated. Every entry point is stream-ordered on
  * `stream`, performs no allocation and no host synchronisation (so a caller may capture it
  * in a hipGraph), keeps no global mutable state and is reentrant: calls on different
- * streams must use different workspaces.
+ * streams must use different workspaces. The one exception is fl_scan_forward_static, whose
+ * look-back state is a per-GPU array inside the library (see its comment).
  *
  * Complex state vectors are stored planar, [B, 2C] floats: the first C entries of a row
  * are the real parts and the next C the imaginary parts (the layout of read[:, t, :2C]).
@@ -48,6 +49,7 @@ extern "C" {
 #define FL_ERR_INVALID_ARGUMENT 1 /* shape / stride / pointer check failed (Python: ValueError) */
 #define FL_ERR_DTYPE 2            /* unsupported raw or read dtype (Python: TypeError) */
 #define FL_ERR_WORKSPACE 3        /* workspace NULL or smaller than fl_scan_workspace_bytes */
+#define FL_ERR_CAPTURE 4          /* fl_scan_forward_static: first call on a device under capture */
 #define FL_ERR_HIP_BASE 1000      /* FL_ERR_HIP_BASE + hipError_t */
 
 /*
@@ -89,6 +91,30 @@ int fl_scan_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_
                     int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,
                     const float* gamma, const float* state_in, float* state_out, void* read,
                     int read_dtype, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * fl_scan_forward without a workspace argument, for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). It has no
+ * counterpart in the reference. It calls no hipMalloc, hipFree or allocating library routine: the
+ * look-back state lives in a file-scope device array of FL_STATIC_SCRATCH_BYTES in this library,
+ * one copy per GPU, held until the process ends.
+ *
+ *   * Shapes: B * ceil(C / 64) * ceil(T / 128) <= FL_STATIC_MAX_TILES (config 2 needs 1,024,
+ *     B = 1 with T = 65,536 and C = 512 needs 4,096); larger shapes return FL_ERR_WORKSPACE.
+ *   * The first call on each device zero-fills that device's array on `stream`: it must not be
+ *     made under stream capture (FL_ERR_CAPTURE). Later calls may be captured.
+ *   * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (two streams,
+ *     two threads) race and must be serialised by the caller.
+ *   * A bounded wait that gives up leaves NaN in the outputs that depend on it (there is no error
+ *     word the caller can read).
+ * Arguments and results as fl_scan_forward (FL_ALGO_AUTO); results are bit-identical to it.
+ */
+#define FL_STATIC_MAX_TILES 12288
+#define FL_STATIC_SCRATCH_BYTES 31508480 /* 2 KiB header + 12,288 status words + tagged words */
+int fl_scan_forward_static(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
+                           int64_t raw_stride_b, int64_t raw_stride_t, const float* tr,
+                           const float* ti, const float* gamma, const float* state_in,
+                           float* state_out, void* read, int read_dtype, void* stream);
 
 /* As fl_scan_forward with an explicit algorithm (FL_ALGO_*). */
 int fl_scan_forward_ex(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
