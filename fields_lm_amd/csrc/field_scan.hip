@@ -120,15 +120,10 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
 
 // Output stores (read, grad_raw) are streamed: written once, never read back by the kernel. The
 // non-temporal hint keeps them from displacing the raw data and the look-back words in the
-// caches (B=1, T=65,536: 150.9 -> 126.3 us; bf16 read and the RMSNorm epilogue at B=8, T=2,048
-// 7 % faster).
+// caches. With the launch's buffers cold (not resident in the 256 MB Infinity Cache from an
+// earlier launch), nt stores beat plain and sc1 stores for every output: B=8, T=2,048, fp32 read
+// 43.1 -> 39.3 us, bf16 read 36.2 -> 34.5 us, RMSNorm epilogue 39.1 -> 36.3 us against sc1.
 constexpr int kStreamStore = 2;  // buffer store cache policy: nt
-// The LDS-staged forward stores instead use sc1 when the launch's raw and read bytes fit in the
-// 256 MB Infinity Cache: then the output stays there for its consumer (the next GEMM), and at
-// B=8, T=2,048 the fp32 read scan takes 32.0 against 32.8 us. Above that size sc1 is much slower
-// (B=12: 54.3 against 46.1 us with nt); the crossover lies between 235 and 277 MB.
-constexpr int kCacheStore = 16;  // buffer store cache policy: sc1
-constexpr int64_t kInfinityCacheBytes = 256ll << 20;
 
 template <typename OutT, int K>
 struct ReadStore;
@@ -349,14 +344,13 @@ struct WaveTile {
   // 16-byte buffer stores. The whole store offset is in voffset, so rows past the descriptor's
   // bound (past T) are dropped by it; the tile's 64 channels must all lie below C.
   static constexpr int kStageRows = L >= 16 ? 4 : 2;  // R
-  template <typename OutT, bool NORM>
+  template <typename OutT, bool NORM, int R = kStageRows>
   __device__ __forceinline__ void materialize_lds(rsrc_t w, int lane, int so0, int row_bytes,
                                                   int plane_bytes, int ch_bytes0, int n,
                                                   float* stage, const float* lr, const float* li,
                                                   float* sr, float* si, float scale,
-                                                  const float (*nw)[K], bool keep) const {
-    constexpr int R = kStageRows;
-    static_assert(K == 1 && L % R == 0, "LDS-staged stores: one channel per lane, whole groups");
+                                                  const float (*nw)[K]) const {
+    static_assert(K == 1 && L % R == 0 && R % 2 == 0, "LDS-staged stores: one channel per lane, whole groups");
 #pragma unroll
     for (int g = 0; g < L / R; ++g) {
 #pragma unroll
@@ -395,11 +389,7 @@ struct WaveTile {
           q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
           q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
           const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
-          if (keep) {
-            __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kCacheStore);
-          } else {
-            __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
-          }
+          __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
         }
       } else {
         // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
@@ -412,11 +402,7 @@ struct WaveTile {
           q.x = bf16_pair(a.x, a.y); q.y = bf16_pair(a.z, a.w);
           q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
           const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
-          if (keep) {
-            __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kCacheStore);
-          } else {
-            __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
-          }
+          __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
         }
       }
     }
@@ -1051,6 +1037,24 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
   }
 }
 
+// Block-order tile of block i with the channel tiles of a row group on one XCD. The dispatcher
+// sends block i to XCD i mod 8, so consecutive tickets (the channel tiles of one row group, the
+// same rows of raw and read) would land on eight XCDs. Within each window of 8 row groups
+// (8 * n_ctiles blocks) the blocks of one XCD instead take the channel tiles of one row group:
+// block w*win + 8*j + x takes ticket w*win + x*n_ctiles + j. Every ticket of a window still comes
+// from a block of that window, so the block-order progress argument holds (a window's blocks
+// are dispatched once the earlier windows' blocks are done, and a window of at most 256 blocks
+// fits the chip); a last partial window keeps identity order. Cold B=8, T=2,048: fp32 read
+// 39.2 -> 38.6 us, bf16 read 34.6 -> 33.3 us. (With the RMSNorm epilogue it is slower, 36.4 ->
+// 39.8 us, and not used there.)
+__device__ __forceinline__ uint32_t xcd_grouped_ticket(uint32_t i, uint32_t n_ctiles, uint32_t n_tiles) {
+  const uint32_t win = 8u * n_ctiles;
+  if (win > 256u) return i;
+  const uint32_t w = i / win, u = i - w * win;
+  if ((w + 1u) * win > n_tiles) return i;
+  return w * win + (u & 7u) * n_ctiles + (u >> 3);
+}
+
 // NORM: out = RMSNorm(read) (canon:300-309 applied to canon:1176-1193's read), norm_w [4C],
 // sib = per-row partials [n_tiles][W*L] words; otherwise out = read and those are unused.
 // LDSIO (bf16 raw, fp32 read, K = 1, every channel tile full, 16-byte aligned raw rows): each
@@ -1064,7 +1068,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
     uint32_t* status, uint64_t* data, uint32_t n_tiles, bool in_order,
-    const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib, bool keep_out) {
+    const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1094,6 +1098,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     // block i takes tile i; the epoch (the counter's high word) is loaded now and stored to LDS
     // once the raw loads issued after it have landed
     ticket = blockIdx.x;
+    if constexpr (!NORM) ticket = xcd_grouped_ticket(ticket, (uint32_t)n_ctiles, n_tiles);
     if (wave == 0)
       epoch_word = __hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
@@ -1297,7 +1302,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
         float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
         tile.template materialize_lds<OutT, true>(io.read, lane, wave * L * io.read_row, io.read_row,
                                                   io.read_plane, ctile * CT * (int)sizeof(OutT),
-                                                  n_valid, stage, lr, li, sr, si, scale, nw, keep_out);
+                                                  n_valid, stage, lr, li, sr, si, scale, nw);
       } else {
         tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
                                              io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
@@ -1307,7 +1312,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
       tile.template materialize_lds<OutT, false>(io.read, lane, wave * L * io.read_row, io.read_row,
                                                  io.read_plane, ctile * CT * (int)sizeof(OutT),
-                                                 n_valid, stage, lr, li, sr, si, 0.f, nullptr, keep_out);
+                                                 n_valid, stage, lr, li, sr, si, 0.f, nullptr);
     } else {
       tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
                                      io.read_plane, n_valid, lr, li, sr, si);
@@ -2300,13 +2305,10 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // start, which the look-back needs to keep up (B=1, T=65,536: 155 us; 203 us in block order,
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
-  // staged stores: keep the output in the Infinity Cache when the launch's bytes fit there
-  const bool keep_out =
-      B * T * (3 * C * (int64_t)sizeof(RawT) + 4 * C * (int64_t)sizeof(OutT)) <= kInfinityCacheBytes;
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
-      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, keep_out);
+      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib);
   return hip_status(hipGetLastError());
 }
 
