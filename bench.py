@@ -116,6 +116,7 @@ def measured_traffic(workload: str, variant: str = "read_fp32"):
 
 INFINITY_CACHE_BYTES = 256 * 2**20
 COLD_SET_BYTES = 1 << 30  # rotated buffer sets add up to at least this: 4x the Infinity Cache
+PREPARE_LAUNCHES = 100  # untimed launches before the warm-up steps of every timed loop
 
 
 def time_plan(plans, steps: int, warmup: int):
@@ -129,6 +130,11 @@ def time_plan(plans, steps: int, warmup: int):
 
     plans = plans if isinstance(plans, (list, tuple)) else [plans]
     stream = torch.cuda.current_stream(plans[0].device)
+    # preparation before the warm-up steps: every buffer set touched and the GPU out of its idle
+    # clocks (the first timed loop of a process otherwise runs about 1 us per launch slower)
+    for i in range(max(PREPARE_LAUNCHES, 4 * len(plans))):
+        plans[i % len(plans)].run(stream)
+    torch.cuda.synchronize()
     for i in range(max(warmup, len(plans))):
         plans[i % len(plans)].run(stream)
     torch.cuda.synchronize()
@@ -374,7 +380,7 @@ def decode_comparison(batch: int = 64, dim: int = 1024, prompt: int = 2048, toke
     }
 
 
-def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
+def backward_timing(workload: str, steps: int = 50, warmup: int = 5, cold_only: bool = False):
     """fl_scan_backward on a workload (bf16 raw and bf16 grad_raw, fp32 read / grad_read):
     algorithmic bytes per token 3C*2 (raw) + 4C*4 (grad_read) + 3C*2 (grad_raw) + 2C*4/8 (the
     read's state at the row before each 8-step wave, from which the kernel recomputes s_{t-1})
@@ -420,7 +426,7 @@ def backward_timing(workload: str, steps: int = 50, warmup: int = 5):
     n_sets = cold_sets(plans[0].nbytes())
     plans += [_Plan(wl.raw.clone()) for _ in range(n_sets - 1)]
     _, ev = time_plan(plans, steps, warmup)
-    _, hot = time_plan(plans[0], steps, warmup)
+    hot = float("nan") if cold_only else time_plan(plans[0], steps, warmup)[1]
     nbytes = (3 * C * 2 + 4 * C * 4 + 3 * C * 2 + 2 * C * 4 // BWD_WAVE_ROWS) * B * T
     if any(nat.workspace_error(p.ws) != 0 for p in plans):
         raise RuntimeError("backward look-back wait gave up")
@@ -670,8 +676,8 @@ def main() -> int:
         print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
         return 0
     if args.backward_only:
-        print(json.dumps({"backward": backward_timing(args.workload, steps=args.steps, warmup=args.warmup)}),
-              flush=True)
+        print(json.dumps({"backward": backward_timing(args.workload, steps=args.steps, warmup=args.warmup,
+                                                      cold_only=args.cold_only)}), flush=True)
         return 0
     if args.model:
         fn = model_prefill if args.model == "prefill" else model_decode
