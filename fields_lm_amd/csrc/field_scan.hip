@@ -849,9 +849,12 @@ __device__ __forceinline__ void report_error(LookbackHeader* hdr, uint32_t bits)
   atomicOr(&hdr->error, bits);
   const unsigned long long h =
       __hip_atomic_load(&hdr->host_error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // through a global-address-space pointer: a store through a generic pointer may write LDS as
+  // far as the compiler knows, and would make every later LDS access of the kernel wait for all
+  // outstanding global loads and stores
   if (h != 0ull)
-    __hip_atomic_store(reinterpret_cast<uint32_t*>(h), bits, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_SYSTEM);
+    __hip_atomic_store(reinterpret_cast<__attribute__((address_space(1))) uint32_t*>(h), bits,
+                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
 
 __device__ __forceinline__ float poison() { return __builtin_nanf(""); }
