@@ -556,8 +556,10 @@ __device__ __forceinline__ void load_params(const float* __restrict__ tr, const 
   }
 }
 
-// Buffer descriptors of one tile: raw from row t_begin of batch row b to the end of row T-1,
-// read over the same rows.
+// Buffer descriptors of one tile: raw from row t_begin of batch row b to the end of the tile's
+// last row (row min(t_begin + span, T) - 1), read over the same rows. Covering only the tile's
+// rows keeps every descriptor below 2 GiB whatever T is (a row is below 4 MiB, a tile at most
+// 128 rows), and rows past T still read as 0 and drop their stores.
 struct TileIo {
   rsrc_t raw, read;
   int vo_raw, vo_read;          // per-lane channel byte offsets
@@ -567,9 +569,9 @@ struct TileIo {
 
 template <typename RawT, typename OutT>
 __device__ __forceinline__ TileIo tile_io(const RawT* raw, int64_t sb, int64_t st, OutT* read,
-                                          int T, int C, int b, int t_begin, int c0) {
+                                          int T, int C, int b, int t_begin, int span, int c0) {
   TileIo io;
-  const int rows = T - t_begin;  // >= 1
+  const int rows = min(T - t_begin, span);  // >= 1
   const RawT* rbase = raw + (int64_t)b * sb + (int64_t)t_begin * st;
   io.raw = make_rsrc(rbase, (uint32_t)(((int64_t)(rows - 1) * st + 3 * (int64_t)C) * sizeof(RawT)));
   OutT* wbase = read + ((int64_t)b * T + t_begin) * 4 * C;
@@ -607,7 +609,7 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_summary_kernel(
 
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
-  const TileIo io = tile_io<RawT, float>(raw, sb, st, nullptr, T, C, b, chunk * kChunkT, c0);
+  const TileIo io = tile_io<RawT, float>(raw, sb, st, nullptr, T, C, b, chunk * kChunkT, kChunkT, c0);
   WaveTile<RawT, K, L> tile;
   tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
   float P[K], Br[K], Bi[K];
@@ -725,7 +727,7 @@ __global__ __launch_bounds__(W * 64) void fl_chunk_materialize_kernel(
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
   const int t_begin = chunk * kChunkT;
-  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, kChunkT, c0);
   WaveTile<RawT, K, L> tile;
   tile.load(io.raw, io.vo_raw, wave * L * io.raw_row, io.raw_row, io.raw_plane, gm);
   const int n = min(max(T - (t_begin + wave * L), 0), L);  // valid steps of this wave
@@ -1134,7 +1136,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 
   float lr[K], li[K], gm[K];
   load_params<K>(tr, ti, gamma, c0, ok, lr, li, gm);
-  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, c0);
+  const TileIo io = tile_io<RawT, OutT>(raw, sb, st, read, T, C, b, t_begin, TC, c0);
   WaveTile<RawT, K, L> tile;
   if constexpr (LDSIO) {
     // this wave's rows: 8 rows of one plane per instruction (lane = 8 * row + 16-byte piece)
@@ -1494,8 +1496,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   const int w0 = t_begin + wave * L;
   const int n_valid = min(max(T - w0, 0), L);
 
-  // buffers from row t_begin of batch row b: raw (rows of st elements), grad_read (rows of 4C)
-  const int rows = T - t_begin;
+  // buffers over the tile's rows from row t_begin of batch row b: raw (rows of st elements),
+  // grad_read (rows of 4C), grad_raw (rows of 3C); rows past T read as 0 and drop their stores
+  const int rows = min(T - t_begin, TC);
   const rsrc_t r_raw = make_rsrc(raw + (int64_t)b * sb + (int64_t)t_begin * st,
                                  (uint32_t)(((int64_t)(rows - 1) * st + 3 * (int64_t)C) * sizeof(RawT)));
   const rsrc_t r_grd = make_rsrc(grad_read + ((int64_t)b * T + t_begin) * 4 * C,
@@ -2373,12 +2376,11 @@ int dispatch_decode(int k, const void* raw_t, int64_t B, int64_t C, int64_t sb, 
 }
 
 // Shape limits: grid.y = C/(64K) and grid.z = B stay <= 65535; the buffer descriptors of a
-// tile (from its first row to the end of its batch row) and every byte offset inside them
+// tile (its rows only, at most 128 rows of at most 4 MiB) and every byte offset inside them
 // stay below 2^31; the look-back tile count stays below 2^31.
 constexpr int64_t kMaxB = 65535;
 constexpr int64_t kMaxC = (int64_t)1 << 16;
 constexpr int64_t kMaxT = (int64_t)1 << 30;
-constexpr int64_t kMaxBufferBytes = ((int64_t)1 << 31) - 1;
 constexpr int64_t kMaxRowBytes = (int64_t)1 << 22;  // 512 rows of a tile stay below 2^31 bytes
 
 size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
@@ -2481,10 +2483,8 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   if (raw_stride_t < 3 * C || raw_stride_b < 0) return FL_ERR_INVALID_ARGUMENT;
   if (B > 1 && raw_stride_b < (T - 1) * raw_stride_t + 3 * C) return FL_ERR_INVALID_ARGUMENT;
   const int64_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
-  // per batch row, raw and read rows are addressed through 32-bit buffer offsets
+  // within a tile, raw and read rows are addressed through 32-bit buffer offsets
   const int64_t osz = read_dtype == FL_DTYPE_BF16 ? 2 : 4;
-  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * osz > kMaxBufferBytes)
-    return FL_ERR_INVALID_ARGUMENT;
   if (raw_stride_t * esz > kMaxRowBytes || 4 * C * osz > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
   if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!raw || !tr || !ti || !gamma || !read) return FL_ERR_INVALID_ARGUMENT;
@@ -2765,8 +2765,6 @@ int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64
   if (B > 1 && raw_stride_b < (T - 1) * raw_stride_t + 3 * C) return FL_ERR_INVALID_ARGUMENT;
   const int64_t esz = raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
   const int64_t gsz = grad_raw_dtype == FL_DTYPE_BF16 ? 2 : 4;
-  if (((T - 1) * raw_stride_t + 3 * C) * esz > kMaxBufferBytes || T * 4 * C * 4 > kMaxBufferBytes)
-    return FL_ERR_INVALID_ARGUMENT;
   if (raw_stride_t * esz > kMaxRowBytes || 4 * C * 4 > kMaxRowBytes) return FL_ERR_INVALID_ARGUMENT;
   if (B * cdiv(T, 32) * cdiv(C, 64) >= ((int64_t)1 << 31)) return FL_ERR_INVALID_ARGUMENT;
   if (!raw || !tr || !ti || !gamma || !read || !grad_read || !grad_raw || !grad_tr || !grad_ti ||
