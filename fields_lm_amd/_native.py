@@ -211,8 +211,9 @@ def workspace_error(ws: torch.Tensor) -> int:
 
 
 # FIELDS_AMD_CHECK=1: every scan, RMSNorm-epilogue scan and backward call synchronizes its stream
-# and raises if one of its look-back waits gave up (not usable under HIP graph capture). Without
-# it a wait that gave up is reported at the next call on the workspace (before_call).
+# and raises if one of its look-back waits gave up (skipped while the stream is capturing a HIP
+# graph, which cannot synchronize). Without it, and for graph replays, a wait that gave up is
+# reported at the next call on the workspace (before_call).
 CHECK_WAITS = os.environ.get("FIELDS_AMD_CHECK", "0") not in ("", "0")
 
 
@@ -220,8 +221,8 @@ def check_waits(ws: torch.Tensor, what: str) -> None:
     """With CHECK_WAITS: raise RuntimeError if the workspace's error word is set (bit 0: a wait
     gave up after its spin limit, so a tile went on without its carry or its partner tiles'
     values; bit 1: a ticket beyond the launch's tiles), then clear the word (and the host word)
-    so that later calls are checked afresh."""
-    if not CHECK_WAITS:
+    so that later calls are checked afresh. A no-op while the current stream is capturing."""
+    if not CHECK_WAITS or (ws.is_cuda and torch.cuda.is_current_stream_capturing()):
         return
     err = workspace_error(ws)
     if err:
