@@ -10,6 +10,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+import weakref
 import threading
 from pathlib import Path
 
@@ -129,13 +130,40 @@ HOST_ERROR_OFFSET = 392
 REZERO_CALLS = 1 << 29
 
 
+class _HostWords:
+    """Pinned host int32 words for the workspaces' failure reports, handed out from pages that are
+    never freed: a kernel that outlives its workspace can only ever write into a word of this pool
+    (whose next owner then sees a spurious failure), never into memory reused for other data."""
+
+    PAGE = 1024
+
+    def __init__(self):
+        self.pages = []
+        self.free = []
+
+    def take(self) -> torch.Tensor:
+        if not self.free:
+            page = torch.zeros(self.PAGE, dtype=torch.int32, pin_memory=True)
+            self.pages.append(page)
+            self.free.extend(page[i:i + 1] for i in range(self.PAGE - 1, -1, -1))
+        word = self.free.pop()
+        word.zero_()
+        return word
+
+    def give(self, word: torch.Tensor) -> None:
+        self.free.append(word)
+
+
+_host_words = _HostWords()
+
+
 class WorkspaceGuard:
     """Host side of one workspace: a pinned host word whose address sits in the header (the
     kernels set it when a bounded wait gives up, so no device read is needed to see it) and the
     count of calls since the workspace was zero-filled."""
 
     def __init__(self, ws: torch.Tensor):
-        self.host_error = torch.zeros(1, dtype=torch.int32, pin_memory=True)
+        self.host_error = _host_words.take()
         self.calls = 0
         self.arm(ws)
 
@@ -159,17 +187,26 @@ class WorkspaceGuard:
             self.calls = 0
 
 
+# Guards by (device, address) of their workspace tensor; an entry leaves with its tensor, so a
+# workspace later allocated at the same address gets a guard (and a header) of its own.
 _guards: dict = {}
 
 
-def guard_workspace(ws: torch.Tensor) -> WorkspaceGuard:
-    """The guard of a zero-filled workspace tensor (created on first use: writes the host word's
-    address into the header)."""
+def _drop_guard(key, guard: WorkspaceGuard) -> None:
+    if _guards.get(key) is guard:
+        del _guards[key]
+    _host_words.give(guard.host_error)
+
+
+def guard_workspace(ws: torch.Tensor, fresh: bool = False) -> WorkspaceGuard:
+    """The guard of a workspace tensor, created (and its host word's address written into the
+    header) on first use. ``fresh``: a newly zero-filled workspace, which always gets a new guard."""
     key = (ws.device.index, ws.data_ptr())
     g = _guards.get(key)
-    if g is None:
+    if g is None or fresh:
         g = WorkspaceGuard(ws)
         _guards[key] = g
+        weakref.finalize(ws, _drop_guard, key, g)
     return g
 
 
@@ -196,11 +233,9 @@ def scan_workspace(device: torch.device, nbytes: int, kind: str = "forward") -> 
     key = (device.index if device.index is not None else torch.cuda.current_device(), stream.cuda_stream, kind)
     ws = _workspaces.get(key)
     if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            _guards.pop((ws.device.index, ws.data_ptr()), None)
         ws = torch.zeros(max(nbytes, 1 << 20), device=device, dtype=torch.uint8)
         _workspaces[key] = ws
-        guard_workspace(ws)
+        guard_workspace(ws, fresh=True)
     return ws
 
 

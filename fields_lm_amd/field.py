@@ -731,7 +731,7 @@ class ScanPlan:
         self.state_out = torch.empty((batch, 2 * channels), device=dev, dtype=torch.float32)
         self.ws_bytes = int(self.lib.fl_scan_workspace_bytes(batch, length, channels))
         self.workspace = torch.zeros(self.ws_bytes, device=dev, dtype=torch.uint8)  # zero-filled once
-        nat.guard_workspace(self.workspace)
+        nat.guard_workspace(self.workspace, fresh=True)
         head = (nat.ptr(raw), nat.dtype_code(raw.dtype), batch, length, channels, raw.stride(0),
                 raw.stride(1), *[nat.ptr(p) for p in self.params], nat.ptr(self.state_in),
                 nat.ptr(self.state_out))

@@ -136,3 +136,43 @@ def test_given_up_backward_wait_poisons_gradients(dev, monkeypatch):
     (out * gread.double().cpu()).sum().backward()
     assert oracle.rel_err(g_raw2.cpu(), r.grad) <= 1e-4
     assert oracle.rel_err(g_tr2.cpu(), p[0].grad) <= 1e-4
+
+
+def test_workspace_at_a_reused_address_has_its_own_guard(dev, monkeypatch):
+    """A plan whose workspace is allocated where a freed plan's workspace was (the caching
+    allocator hands the block back) gets a guard of its own: its header names its own host word,
+    and a forced give-up on it is reported at its next call."""
+    import gc
+
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd import _native as nat
+
+    monkeypatch.setattr(nat, "CHECK_WAITS", False)
+    B, T, C = 1, 66 * 128, 64
+    print(f"[case] reused workspace address B={B} T={T} C={C}", flush=True)
+    g = torch.Generator().manual_seed(23)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, seed=5))
+    plan = ScanPlan(raw, tr, ti, gamma)
+    plan.run()
+    torch.cuda.synchronize()
+    first = plan.workspace.data_ptr()
+    del plan
+    gc.collect()
+    plan = ScanPlan(raw, tr, ti, gamma)
+    ws = plan.workspace
+    guard = nat._guards[(dev.index, ws.data_ptr())]
+    named = int(ws[392:400].cpu().view(torch.int64).item())
+    assert named == guard.host_error.data_ptr() and guard.calls == 0
+    print(f"[case] same address as the freed plan: {ws.data_ptr() == first}", flush=True)
+    _seed_counter(ws, epoch=3, first_ticket=66 - 1)
+    nat.set_spin_limit(ws, 16)
+    plan.run()
+    torch.cuda.synchronize()
+    with pytest.raises(RuntimeError, match="wait give up"):
+        plan.run()
+    nat.set_spin_limit(ws, 0)
+    out = plan.run()
+    torch.cuda.synchronize()
+    exp, _ = oracle.scan_f64(raw.float().cpu(), tr.cpu(), ti.cpu(), gamma.cpu())
+    assert oracle.rel_err(out.cpu(), exp) <= 1e-4
