@@ -111,3 +111,43 @@ def test_random_shape_against_oracle(dev, i):
         assert oracle.rel_err(g_gm.cpu(), p[2].grad) <= 1e-4
         if s0 is not None:
             assert oracle.rel_err(g_sin.cpu(), s0.grad) <= 1e-4
+
+
+@pytest.mark.parametrize("i", range(24))
+def test_random_decode_step_against_oracle(dev, i):
+    """Random B (1..300), C (1..1200), raw dtype, padded raw_t rows and output dtype: two chained
+    steps of ``field_decode_step`` and of ``field_decode_norm_step`` against ``decode_step_f64``
+    (+ ``rms_norm_f64``), state included, at 1e-4 (bf16 output: 1e-2)."""
+    from fields_lm_amd import field_decode_norm_step, field_decode_step
+
+    rng = np.random.default_rng(5000 + i)
+    B, C = int(rng.integers(1, 301)), int(rng.integers(1, 1201))
+    pad = int(rng.choice([0, 8, int(rng.integers(1, 17))]))
+    raw_bf16, out_bf16 = bool(rng.integers(0, 2)), bool(rng.integers(0, 3) == 0)
+    eps = float(rng.choice([1e-6, 0.05]))
+    print(f"[case] decode fuzz {i}: B={B} C={C} pad={pad} raw_bf16={raw_bf16} out_bf16={out_bf16}",
+          flush=True)
+    g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+    rl, th = ref.init_radius_theta(C)
+    tr, ti, gamma = ref.transition_params(rl + 0.5 * torch.randn(C, generator=g),
+                                          th + 0.3 * torch.randn(C, generator=g))
+    w = torch.rand(4 * C, generator=g) + 0.5
+    state0 = torch.randn(B, 2 * C, generator=g)
+    d = [t.to(dev) for t in (tr, ti, gamma)]
+    st_plain, st_norm = state0.to(dev), state0.to(dev)
+    exp_state = state0.double().numpy()
+    for step in range(2):
+        full = torch.randn(B, 3 * C + pad, generator=g) * 2
+        if raw_bf16:
+            full = full.to(torch.bfloat16)
+        raw_cpu = full[:, :3 * C].float()
+        raw_t = full.to(dev)[:, :3 * C]  # row stride 3C + pad
+        read_t = field_decode_step(raw_t, *d, st_plain)
+        normed = field_decode_norm_step(raw_t, *d, st_norm, w.to(dev), eps,
+                                        out_dtype=torch.bfloat16 if out_bf16 else torch.float32)
+        exp_read, exp_state = oracle.decode_step_f64(raw_cpu, tr, ti, gamma, exp_state)
+        assert oracle.rel_err(read_t.cpu(), exp_read) <= 1e-4, step
+        exp_norm = oracle.rms_norm_f64(exp_read, w, eps)
+        assert oracle.rel_err(normed.float().cpu(), exp_norm) <= (1e-2 if out_bf16 else 1e-4), step
+        assert oracle.rel_err(st_plain.cpu(), exp_state) <= 1e-4, step
+        assert torch.equal(st_plain, st_norm), step  # the same state update in both kernels
