@@ -9,7 +9,7 @@ times the torch restatement of the reference's CPU path (oracle/reference_path.p
 host's cores on the same workload.
 
     python bench.py [--steps K] [--warmup W] [--workload NAME] [--variant V] [--no-cpu-baseline]
-                    [--no-extras] [--decode-only]
+                    [--no-extras] [--decode-only] [--copy-ceilings]
 
 ``--variant`` picks the timed scan: read_fp32 (the headline: fp32 read, 11,264 B/token),
 read_bf16 (7,168 B/token), norm_bf16 / norm_fp32 (read_norm fused into the epilogue).
@@ -192,6 +192,83 @@ def scan_timing(wl, kw: dict, steps: int, warmup: int) -> dict:
             "frac_hbm_peak": nb / (cold * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "hot_us_per_step": hot * 1e3, "hot_frac_hbm_peak": nb / (hot * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "cache": f"cold: {n_sets} rotated buffer sets; hot: one set replayed"}
+
+
+class _CopyPlan:
+    """One measurement copy (``libfields_bench.so``) over one buffer set, with the ``run(stream)``
+    and ``device`` of a ScanPlan so that :func:`time_plan` times it the same way."""
+
+    def __init__(self, lib, kind: str, raw, out, out_elem_bytes: int):
+        self.lib, self.kind, self.raw, self.out, self.osz = lib, kind, raw, out, out_elem_bytes
+        self.device = raw.device
+
+    def run(self, stream=None):
+        import ctypes
+
+        import torch
+
+        s = stream if stream is not None else torch.cuda.current_stream(self.device)
+        h = ctypes.c_void_p(s.cuda_stream)
+        B, T, C3 = self.raw.shape
+        if self.kind == "tile":
+            rc = self.lib.fl_bench_tile_copy(ctypes.c_void_p(self.raw.data_ptr()),
+                                             ctypes.c_void_p(self.out.data_ptr()), B, T, C3 // 3,
+                                             self.osz, h)
+        else:
+            rc = self.lib.fl_bench_stream_copy(ctypes.c_void_p(self.raw.data_ptr()),
+                                               ctypes.c_void_p(self.out.data_ptr()),
+                                               self.raw.numel() * self.raw.element_size(),
+                                               self.out.numel(), h)
+        if rc != 0:
+            raise RuntimeError(f"copy kernel {self.kind}: error {rc}")
+
+
+def copy_ceilings(wl, scan_us: dict, steps: int = 100, warmup: int = 10) -> dict:
+    """Cold copy ceilings of the scan's byte mix on this box, beside the scan's own cold time:
+    ``fl_bench_tile_copy`` (the scan's access pattern, tiles, grid, occupancy and tile order,
+    without its arithmetic or look-back) and ``fl_bench_stream_copy`` (a streaming copy of the
+    same bytes), for the fp32 and the bf16 read; buffer sets rotated as for the scan."""
+    import ctypes
+
+    import torch
+
+    from fields_lm_amd.build import BENCH_LIB_PATH
+
+    if not BENCH_LIB_PATH.exists():
+        return {"skipped": f"{BENCH_LIB_PATH.name} not built (python -m fields_lm_amd.build)"}
+    lib = ctypes.CDLL(str(BENCH_LIB_PATH))
+    lib.fl_bench_tile_copy.restype = ctypes.c_int
+    lib.fl_bench_tile_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 + \
+        [ctypes.c_int, ctypes.c_void_p]
+    lib.fl_bench_stream_copy.restype = ctypes.c_int
+    lib.fl_bench_stream_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                         ctypes.c_size_t, ctypes.c_void_p]
+    B, T, C3 = wl.raw.shape
+    C = C3 // 3
+    if T % 128 or C % 64 or wl.raw.element_size() != 2:
+        return {"skipped": "the tile pattern needs bf16 raw, T % 128 == 0 and C % 64 == 0"}
+    out = {}
+    for key, osz in (("fp32_read", 4), ("bf16_read", 2)):
+        raw_bytes = wl.raw.numel() * wl.raw.element_size()
+        out_bytes = B * T * 4 * C * osz
+        n_sets = cold_sets(raw_bytes + out_bytes)
+        raws = [wl.raw] + [wl.raw.clone() for _ in range(n_sets - 1)]
+        outs = [torch.empty(out_bytes, device=wl.raw.device, dtype=torch.uint8) for _ in range(n_sets)]
+        res = {"bytes": raw_bytes + out_bytes, "scan_us": scan_us[key]}
+        for kind in ("tile", "stream"):
+            plans = [_CopyPlan(lib, kind, r, o, osz) for r, o in zip(raws, outs)]
+            _, ms = time_plan(plans, steps, warmup)
+            name = "tile_pattern" if kind == "tile" else "streaming"
+            res[f"{name}_us"] = ms * 1e3
+            res[f"{name}_frac_hbm_peak"] = (raw_bytes + out_bytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS
+            if scan_us[key] is not None:
+                res[f"scan_over_{name}"] = scan_us[key] / (ms * 1e3)
+        out[key] = res
+        del raws, outs
+        torch.cuda.empty_cache()
+    out["note"] = ("cold, HIP events; the scan's time over a copy of its own access pattern "
+                   "(scan_over_tile_pattern) and over a streaming copy of the same bytes")
+    return out
 
 
 def cpu_model() -> str:
@@ -652,6 +729,8 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a 256 MiB device copy (counter calibration for rocprofv3 --pmc)")
+    ap.add_argument("--copy-ceilings", action="store_true",
+                    help="only time the copy kernels of the scan's access pattern (cold)")
     args = ap.parse_args()
     if args.copy_calibration:
         return copy_calibration()
@@ -674,6 +753,12 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.decode_only:
         print(json.dumps({"decode_b64": decode_comparison()}), flush=True)
+        return 0
+    if args.copy_ceilings:
+        wl = make_scan_workload(args.workload, dev)
+        print(json.dumps({"copy_ceilings": copy_ceilings(wl, {"fp32_read": None, "bf16_read": None},
+                                                         steps=args.steps, warmup=args.warmup)}),
+              flush=True)
         return 0
     if args.backward_only:
         print(json.dumps({"backward": backward_timing(args.workload, steps=args.steps, warmup=args.warmup,
@@ -775,6 +860,9 @@ def main() -> int:
                         ("fused_read_norm_bf16_out", dict(read_dtype=torch.bfloat16, norm_weight=w)),
                         ("fused_read_norm_fp32_out", dict(norm_weight=w))]:
             extras[key] = scan_timing(wl, kw, 100, 10)
+        extras["copy_ceilings"] = copy_ceilings(
+            wl, {"fp32_read": ev_ms * 1e3 if args.variant == "read_fp32" else None,
+                 "bf16_read": extras["bf16_read"]["us_per_step"]})
         wll = make_scan_workload("scan_b1_t65536_d1024", dev)
         extras["long_context_fused_read_norm_bf16_out"] = scan_timing(
             wll, dict(read_dtype=torch.bfloat16, norm_weight=torch.ones(4 * wll.channels, device=dev)), 20, 3)

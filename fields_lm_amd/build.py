@@ -20,6 +20,10 @@ REPO_DIR = PKG_DIR.parent
 SOURCES = [PKG_DIR / "csrc" / "field_scan.hip"]
 INCLUDE_DIR = REPO_DIR / "include"
 LIB_PATH = PKG_DIR / "libfields_amd.so"
+# measurement kernels for bench.py (the scan's access pattern without its arithmetic), kept out of
+# the library behind the C ABI
+BENCH_SOURCES = [PKG_DIR / "csrc" / "copy_ceiling.hip"]
+BENCH_LIB_PATH = PKG_DIR / "libfields_bench.so"
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep v_pk_{add,mul,fma}_f32 out of the generated code (the compiler would
@@ -44,12 +48,13 @@ def hipcc() -> str:
     return found
 
 
-def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None) -> Path:
+def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path | None = None,
+          sources: list[Path] | None = None) -> Path:
     """Compile the HIP sources into ``libfields_amd.so`` (always recompiles)."""
     target = Path(out) if out is not None else LIB_PATH
     tmp = target.with_suffix(".so.tmp")
     cmd = [hipcc(), *HIP_FLAGS, *(extra_flags or []), f"-I{INCLUDE_DIR}",
-           *[str(s) for s in SOURCES], "-o", str(tmp)]
+           *[str(s) for s in (sources or SOURCES)], "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     env = dict(os.environ)
@@ -62,5 +67,11 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
     return target
 
 
+def build_bench(verbose: bool = False) -> Path:
+    """Compile the measurement kernels of bench.py into ``libfields_bench.so``."""
+    return build(verbose=verbose, out=BENCH_LIB_PATH, sources=BENCH_SOURCES)
+
+
 if __name__ == "__main__":
     print(build(verbose=True))
+    print(build_bench(verbose=True))

@@ -171,3 +171,20 @@ def test_wait_check_raises_on_error_word(monkeypatch):
     ws[128] = 1
     nat.check_waits(ws, "fl_scan_forward")
     assert nat.workspace_error(ws) == 1
+
+
+def test_bench_library_exports():
+    """bench.py's measurement library (copy kernels of the scan's access pattern) loads and
+    exports its two entry points; its argument checks refuse shapes outside the pattern."""
+    from fields_lm_amd import build
+
+    if not build.BENCH_LIB_PATH.exists():
+        build.build_bench()
+    blib = ctypes.CDLL(str(build.BENCH_LIB_PATH))
+    for name in ("fl_bench_tile_copy", "fl_bench_stream_copy"):
+        assert hasattr(blib, name), name
+    blib.fl_bench_tile_copy.restype = ctypes.c_int
+    blib.fl_bench_tile_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 + \
+        [ctypes.c_int, ctypes.c_void_p]
+    assert blib.fl_bench_tile_copy(None, None, 1, 100, 64, 4, None) == 1  # T % 128 != 0
+    assert blib.fl_bench_tile_copy(None, None, 1, 128, 65, 4, None) == 1  # C % 64 != 0
