@@ -63,8 +63,24 @@ def build(verbose: bool = False, extra_flags: list[str] | None = None, out: Path
         raise RuntimeError(f"hipcc failed ({proc.returncode}):\n{proc.stdout}\n{proc.stderr}")
     if verbose and proc.stderr.strip():
         print(proc.stderr, file=sys.stderr)
+    missing = unresolved_kernel_stubs(tmp)
+    if missing:
+        tmp.unlink()
+        raise RuntimeError(f"{target.name}: hipcc left {len(missing)} kernel launch stub(s) undefined, "
+                           f"so the library would not load: {missing[0]}")
     os.replace(tmp, target)
     return target
+
+
+def unresolved_kernel_stubs(lib: Path) -> list[str]:
+    """Undefined host-side kernel launch stubs of a built library (``nm -D --undefined-only``).
+    hipcc can link a library whose launches refer to stubs it never emitted; dlopen then fails.
+    Empty when nm is absent."""
+    nm = shutil.which("nm")
+    if nm is None:
+        return []
+    proc = subprocess.run([nm, "-D", "--undefined-only", str(lib)], capture_output=True, text=True)
+    return [ln.split()[-1] for ln in proc.stdout.splitlines() if "__device_stub__" in ln]
 
 
 def build_bench(verbose: bool = False) -> Path:

@@ -65,47 +65,47 @@ __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w 
 __device__ __forceinline__ float raw_value(float x) { return x; }
 __device__ __forceinline__ float raw_value(bf16_bits x) { return __uint_as_float((uint32_t)x << 16); }
 
-// raw: buffer load at (voffset, soffset) bytes
-template <typename RawT, int K>
+// raw (and grad_read): buffer load at (voffset, soffset) bytes with cache policy POL
+template <typename RawT, int K, int POL = 0>
 struct RawLoad;
-template <>
-struct RawLoad<float, 1> {
+template <int POL>
+struct RawLoad<float, 1, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    o[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0));
+    o[0] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, vo, so, POL));
   }
 };
-template <>
-struct RawLoad<float, 2> {
+template <int POL>
+struct RawLoad<float, 2, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, POL);
     o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
   }
 };
-template <>
-struct RawLoad<float, 4> {
+template <int POL>
+struct RawLoad<float, 4, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, 0);
+    const u32x4 w = __builtin_amdgcn_raw_buffer_load_b128(r, vo, so, POL);
     o[0] = __uint_as_float(w.x); o[1] = __uint_as_float(w.y);
     o[2] = __uint_as_float(w.z); o[3] = __uint_as_float(w.w);
   }
 };
-template <>
-struct RawLoad<bf16_bits, 1> {
+template <int POL>
+struct RawLoad<bf16_bits, 1, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    o[0] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, 0) << 16);
+    o[0] = __uint_as_float((uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, vo, so, POL) << 16);
   }
 };
-template <>
-struct RawLoad<bf16_bits, 2> {
+template <int POL>
+struct RawLoad<bf16_bits, 2, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, 0);
+    const uint32_t w = __builtin_amdgcn_raw_buffer_load_b32(r, vo, so, POL);
     o[0] = bf16_lo(w); o[1] = bf16_hi(w);
   }
 };
-template <>
-struct RawLoad<bf16_bits, 4> {
+template <int POL>
+struct RawLoad<bf16_bits, 4, POL> {
   __device__ __forceinline__ static void run(rsrc_t r, int vo, int so, float* o) {
-    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, 0);
+    const u32x2 w = __builtin_amdgcn_raw_buffer_load_b64(r, vo, so, POL);
     o[0] = bf16_lo(w.x); o[1] = bf16_hi(w.x); o[2] = bf16_lo(w.y); o[3] = bf16_hi(w.y);
   }
 };
@@ -124,6 +124,18 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
 // earlier launch), nt stores beat plain and sc1 stores for every output: B=8, T=2,048, fp32 read
 // 43.1 -> 39.3 us, bf16 read 36.2 -> 34.5 us, RMSNorm epilogue 39.1 -> 36.3 us against sc1.
 constexpr int kStreamStore = 2;  // buffer store cache policy: nt
+// The LDS-staged raw loads are non-temporal too where the output is bf16 (bf16 read, the RMSNorm
+// epilogue), and plain where it is fp32. Cold, B=8, T=2,048: bf16 read 32.3 -> 31.6 us, RMSNorm
+// epilogue 36.1 -> 34.5 us, B=1, T=65,536: 119.6 -> 117.4 and 150.1 -> 143.0 us; with raw just
+// written by a preceding kernel (as the mixer's projection leaves it) unchanged (29.7 -> 30.0,
+// 36.9 -> 37.0 us). A copy with the scan's tile pattern and fp32 output runs slower with them
+// (35.5 -> 37.0 us). The policy is a constant expression in the kernel itself: passed to the
+// load builtin as a call of a constexpr function template, it left the host stubs of those
+// kernel instances unemitted (the library then fails to load).
+// The backward's grad_read loads (its largest input, read once) are non-temporal: cold, B=8,
+// T=2,048 64.9 -> 60.6 us, B=1, T=65,536 235.4 -> 233.0 us; its raw loads stay plain (nt on
+// them as well: 61.5 and 230.2 us).
+constexpr int kStreamLoad = 2;  // buffer load cache policy: nt
 
 template <typename OutT, int K>
 struct ReadStore;
@@ -1141,12 +1153,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   if constexpr (LDSIO) {
     // this wave's rows: 8 rows of one plane per instruction (lane = 8 * row + 16-byte piece)
     const int vo = ctile * CT * (int)sizeof(RawT) + (lane >> 3) * io.raw_row + (lane & 7) * 16;
+    constexpr int kRawPolicy = sizeof(OutT) == 2 ? kStreamLoad : 0;  // nt for bf16 output
 #pragma unroll
     for (int q = 0; q < 3 * (L / 8); ++q) {
       const int plane = q / (L / 8), r0 = wave * L + (q % (L / 8)) * 8;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           io.raw, (__attribute__((address_space(3))) void*)&s_io[(plane * TC + r0) * CT], 16, vo,
-          r0 * io.raw_row + plane * io.raw_plane, 0, 0);
+          r0 * io.raw_row + plane * io.raw_plane, 0, kRawPolicy);
     }
     __builtin_amdgcn_s_waitcnt(0);  // the wave reads only the rows it staged itself
     tile.load_lds(&s_io[wave * L * CT], TC * CT, lane, gm);
@@ -1515,10 +1528,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 #pragma unroll
   for (int j = 0; j < L; ++j) {
     const int so = (wave * L + j) * grd_row;
-    RawLoad<float, K>::run(r_grd, vo_f, so, uR[j]);
-    RawLoad<float, K>::run(r_grd, vo_f, so + f_plane, uI[j]);
-    RawLoad<float, K>::run(r_grd, vo_f, so + 2 * f_plane, dR[j]);
-    RawLoad<float, K>::run(r_grd, vo_f, so + 3 * f_plane, dI[j]);
+    RawLoad<float, K, kStreamLoad>::run(r_grd, vo_f, so, uR[j]);
+    RawLoad<float, K, kStreamLoad>::run(r_grd, vo_f, so + f_plane, uI[j]);
+    RawLoad<float, K, kStreamLoad>::run(r_grd, vo_f, so + 2 * f_plane, dR[j]);
+    RawLoad<float, K, kStreamLoad>::run(r_grd, vo_f, so + 3 * f_plane, dI[j]);
     float zv[K];
     RawLoad<RawT, K>::run(r_raw, vo_raw, (wave * L + j) * raw_row + 2 * raw_plane, zv);
 #pragma unroll

@@ -44,6 +44,15 @@ def test_library_exports_every_declared_symbol(lib):
         assert name in nat.SIGNATURES, name
 
 
+def test_no_kernel_launch_stub_left_undefined(lib):
+    """Every kernel launch in the library has its host stub: hipcc once linked a library whose
+    launches of four look-back instances referred to stubs it never emitted, and loading it
+    failed. build() refuses such a library."""
+    from fields_lm_amd import build
+
+    assert build.unresolved_kernel_stubs(nat.LIB_PATH) == []
+
+
 def test_header_constants_match_binding():
     text = HEADER.read_text()
     consts = dict(re.findall(r"#define (FL_[A-Z0-9_]+) (\d+)", text))
