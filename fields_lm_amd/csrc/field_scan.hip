@@ -843,7 +843,6 @@ struct LookbackHeader {
 constexpr uint32_t kTagAgg = 1u;
 constexpr uint32_t kTagIncl = 2u;
 constexpr uint32_t kTagSib = 3u;   // per-row partial sum of squares (NORM epilogue)
-constexpr uint32_t kTagPart = 3u;  // backward: parameter-gradient partials and segment totals
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr size_t kHeaderBytes = 2048;
 static_assert(sizeof(LookbackHeader) <= kHeaderBytes, "header region too small");
@@ -1364,8 +1363,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 //   dv  = Re(conj(D) lam p) - Re(conj(G) lam p) + gamma Re(conj(G) inj),  dzv = dv v (1 - v/0.9),
 //   dlam += (1 - v) G conj(p) + v D conj(p),   dgamma += v Re(conj(G) inj),
 // and c_{-1} = grad_state_in. Parameter gradients are summed per tile (each lane over its steps,
-// then the waves in order) into per-tile partials, which the same launch adds up over the tiles of
-// each channel tile in a fixed order (segments of rows, then the segment totals; deterministic).
+// then the waves in order) into per-tile partials, which a second launch
+// (fl_param_grad_reduce_kernel) adds up over the tiles of each channel tile in a fixed order
+// (deterministic).
 // The second pass needs s_{t-1} at every step, which the reference reads back from the forward's
 // read (canon:841-850); here each wave recomputes it with the forward recurrence from the state
 // entering its first row (the read at the row before, state_in or 0 at the sequence start),
@@ -1374,70 +1374,6 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 // staged in LDS by 16-byte buffer loads that write LDS directly, issued with the first pass's
 // loads, so that no load latency follows the look-back.
 // ------------------------------------------------------------------------------------------
-// Two sums over rows of tagged-word matrices (rows of 3 planes of CT words, each base at this
-// lane's first word): rows a0 .. a1-1 of A into acc_a and rows b0 .. b1-1 of B into acc_b, each
-// word awaited until it carries `tag`. Wave w adds rows a0+w, a0+w+W, ... of A in that order into
-// acc_a[w], and likewise for B (the caller adds the waves in order after a barrier), so the sums do
-// not depend on timing. A wave loads kSumRows of its rows of both matrices at a time. Lanes past C
-// (`ok` false) neither wait nor add.
-template <int K, int W>
-__device__ __forceinline__ void sum_tagged_rows(uint64_t* base_a, int a0, int a1, uint64_t* base_b,
-                                                int b0, int b1, uint32_t tag, bool ok, int lane,
-                                                int wave, LookbackHeader* hdr, uint32_t limit,
-                                                float (&acc_a)[W][3][64 * K],
-                                                float (&acc_b)[W][3][64 * K]) {
-  constexpr int CT = 64 * K;
-  constexpr int kSumRows = 4;
-  float sa[3][K], sb[3][K];
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
-#pragma unroll
-    for (int k = 0; k < K; ++k) { sa[p][k] = 0.f; sb[p][k] = 0.f; }
-  uint32_t spins = 0;
-  bool failed = false;
-  // settle rows r of one matrix (loaded as w) and add them in order
-  auto settle_add = [&](uint64_t* base, int r, int r_end, uint64_t (&w)[3][K], float (&acc)[3][K]) {
-    if (r >= r_end || failed) return;
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      uint64_t ww[3] = {w[0][k], w[1][k], w[2][k]};
-      if (!settle_words<3>(base + (size_t)r * 3 * CT + k, CT, tag, ww, spins, limit)) {
-        failed = true;
-        return;
-      }
-      acc[0][k] += word_value(ww[0]);
-      acc[1][k] += word_value(ww[1]);
-      acc[2][k] += word_value(ww[2]);
-    }
-  };
-  for (int i = wave; ok && !failed && (a0 + i < a1 || b0 + i < b1); i += kSumRows * W) {
-    uint64_t wa[kSumRows][3][K], wb[kSumRows][3][K];  // rows i, i + W, ... of A and B
-#pragma unroll
-    for (int q = 0; q < kSumRows; ++q) {
-      const int ra = a0 + i + q * W, rb = b0 + i + q * W;
-#pragma unroll
-      for (int p = 0; p < 3; ++p)
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          wa[q][p][k] = ra < a1 ? get_word(base_a + (size_t)ra * 3 * CT + p * CT + k) : 0ull;
-          wb[q][p][k] = rb < b1 ? get_word(base_b + (size_t)rb * 3 * CT + p * CT + k) : 0ull;
-        }
-    }
-#pragma unroll
-    for (int q = 0; q < kSumRows; ++q) settle_add(base_a, a0 + i + q * W, a1, wa[q], sa);
-#pragma unroll
-    for (int q = 0; q < kSumRows; ++q) settle_add(base_b, b0 + i + q * W, b1, wb[q], sb);
-  }
-  if (__ballot(failed) != 0ull && lane == 0) report_error(hdr, 1u);
-#pragma unroll
-  for (int p = 0; p < 3; ++p)
-#pragma unroll
-    for (int k = 0; k < K; ++k) {  // a sum that missed a row is poisoned
-      acc_a[wave][p][lane * K + k] = failed ? poison() : sa[p][k];
-      acc_b[wave][p][lane * K + k] = failed ? poison() : sb[p][k];
-    }
-}
-
 template <typename RawT, typename GradT, int K, int L, int W, int OCC, bool PF = false>
 __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const RawT* __restrict__ raw, int64_t sb, int64_t st, int T, int C, int n_chunks,
@@ -1447,8 +1383,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
     float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
-    uint64_t* part, uint64_t* segw, int seg_rows, uint32_t n_tiles, uint32_t n_chains,
-    bool in_order) {
+    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1794,63 +1729,66 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     s_part[wave][2][lane * K + k] = ggm[k];
   }
   __syncthreads();
-  // The tiles of a channel tile, in ticket order, are its rows r = ord * B + b. Each publishes
-  // its partials as tagged words (row r of `part`); the last row of each segment of seg_rows rows
-  // adds the segment's rows and publishes the total (row of `segw`); the channel tile's last row
-  // adds its own segment's rows and the earlier segments' totals into grad_tr/ti/gamma. Every
-  // wait is on lower tickets, and every sum runs in a fixed order (sum_tagged_rows, then the
-  // waves in order): the gradients do not depend on timing.
-  const int n_b = (int)(n_chains / (uint32_t)n_ctiles);
-  const int n_rows = n_chunks * n_b;
-  const int row = ord * n_b + b;
-  const int n_seg = (n_rows + seg_rows - 1) / seg_rows;
-  const int seg = row / seg_rows;
-  const int r_end = min((seg + 1) * seg_rows, n_rows);
-  const uint32_t tag_part = ((epoch & 0x3fffffffu) << 2) | kTagPart;
-  uint64_t* pw = part + (size_t)ctile * n_rows * 3 * CT + lane * K;
-  uint64_t* sw = segw + (size_t)ctile * n_seg * 3 * CT + lane * K;
-  if (wave == 0 && ok) {
-#pragma unroll
-    for (int k = 0; k < K; ++k) {
-      const int x = lane * K + k;
-      float a0 = 0.f, a1 = 0.f, a2 = 0.f;
-      for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
-      put_word(pw + (size_t)row * 3 * CT + k, a0, tag_part);
-      put_word(pw + (size_t)row * 3 * CT + CT + k, a1, tag_part);
-      put_word(pw + (size_t)row * 3 * CT + 2 * CT + k, a2, tag_part);
-    }
-  }
-  if (row == r_end - 1) {  // block-uniform: this tile closes its segment
-    // the channel tile's last row adds the earlier segments' totals in the same pass and never
-    // publishes its own segment's total
-    const bool last = row == n_rows - 1;
-    __syncthreads();  // s_part is read and the wave maps in s_sum are used: both hold wave sums now
-    sum_tagged_rows<K, W>(pw, seg * seg_rows, r_end, sw, 0, last ? seg : 0, tag_part, ok, lane, wave,
-                          hdr, limit, s_part, s_sum);
-    __syncthreads();
+  // The tiles of a channel tile, in ticket order, are its rows r = ord * B + b: the tile writes its
+  // row of partials (part[ctile][plane][r][CT]), which fl_param_grad_reduce_kernel adds up after
+  // this launch.
+  {
+    const int n_b = (int)(n_chains / (uint32_t)n_ctiles);
+    const int n_rows = n_chunks * n_b;
+    const int row = ord * n_b + b;
     if (wave == 0 && ok) {
 #pragma unroll
       for (int k = 0; k < K; ++k) {
         const int x = lane * K + k;
         float a0 = 0.f, a1 = 0.f, a2 = 0.f;
         for (int u = 0; u < W; ++u) { a0 += s_part[u][0][x]; a1 += s_part[u][1][x]; a2 += s_part[u][2][x]; }
-        if (!last) {
-          put_word(sw + (size_t)seg * 3 * CT + k, a0, tag_part);
-          put_word(sw + (size_t)seg * 3 * CT + CT + k, a1, tag_part);
-          put_word(sw + (size_t)seg * 3 * CT + 2 * CT + k, a2, tag_part);
-        } else {
-          float e0 = 0.f, e1 = 0.f, e2 = 0.f;  // totals of the segments before this one
-          for (int u = 0; u < W; ++u) { e0 += s_sum[u][0][x]; e1 += s_sum[u][1][x]; e2 += s_sum[u][2][x]; }
-          grad_tr[c0 + k] = e0 + a0;
-          grad_ti[c0 + k] = e1 + a1;
-          grad_gamma[c0 + k] = e2 + a2;
-        }
+        float* pr = part + ((size_t)ctile * 3 * n_rows + row) * CT + x;
+        pr[0] = a0;
+        pr[(size_t)n_rows * CT] = a1;
+        pr[(size_t)2 * n_rows * CT] = a2;
       }
     }
   }
 
   // the last block of the launch re-arms the counter for the next launch (next epoch)
   if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
+}
+
+// Parameter gradients (dlam = grad_tr + i grad_ti and dgamma, summed over batch rows and steps):
+// the backward's per-tile partials part[ctile][plane][row][64] (plane 0: Re dlam, 1: Im dlam,
+// 2: dgamma) added up over the n_rows rows of each channel tile. One block per (channel tile,
+// plane), lane = channel: wave w adds its run of rows in order, then wave 0 adds the 16 wave sums
+// in order, so the sums do not depend on timing.
+__global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float* __restrict__ part,
+                                                                   int n_rows, int C,
+                                                                   float* __restrict__ grad_tr,
+                                                                   float* __restrict__ grad_ti,
+                                                                   float* __restrict__ grad_gamma) {
+  constexpr int CT = 64, NW = 16, kBatch = 32;
+  __shared__ float s_acc[NW][CT];
+  const int lane = threadIdx.x & 63;
+  const int wave = uniform(threadIdx.x >> 6);
+  const int ctile = (int)blockIdx.x / 3, plane = (int)blockIdx.x - 3 * ctile;
+  const float* base = part + ((size_t)ctile * 3 + plane) * n_rows * CT + lane;
+  const int rpw = (n_rows + NW - 1) / NW;
+  const int r0 = min(wave * rpw, n_rows), r1 = min(r0 + rpw, n_rows);
+  float acc = 0.f;
+  for (int r = r0; r < r1; r += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q) v[q] = r + q < r1 ? base[(size_t)(r + q) * CT] : 0.f;
+#pragma unroll
+    for (int q = 0; q < kBatch; ++q)
+      if (r + q < r1) acc += v[q];
+  }
+  s_acc[wave][lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    float t = 0.f;
+    for (int u = 0; u < NW; ++u) t += s_acc[u][lane];
+    const int c = ctile * CT + lane;
+    if (c < C) (plane == 0 ? grad_tr : plane == 1 ? grad_ti : grad_gamma)[c] = t;
+  }
 }
 
 // ------------------------------------------------------------------------------------------
@@ -2405,12 +2343,11 @@ size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
 // workspace: [header 2 KiB][status: tiles x u32][data: tiles x 5 x CT x u64]
 // [partials: tiles x 3 x CT x u64][segment totals: channel tiles x segments x 3 x CT x u64]
 constexpr LookbackTiling kBwdTiling = {1, 8, 8, 4};
-constexpr int kMinSegRows = 16;
 
 struct BwdLayout {
   LookbackGeom g;
-  int n_seg, seg_rows;  // segments of the parameter-gradient reduction and rows per segment
-  size_t status_off, data_off, part_off, seg_off, bytes;
+  int n_rows;  // partial rows per channel tile (tiles of the channel tile: n_chunks x B)
+  size_t status_off, data_off, part_off, bytes;
 };
 
 BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
@@ -2420,15 +2357,8 @@ BwdLayout bwd_layout(int64_t B, int64_t T, int64_t C) {
   w.status_off = kHeaderBytes;
   w.data_off = w.status_off + (size_t)cdiv((int64_t)w.g.n_tiles * 4, 256) * 256;
   w.part_off = w.data_off + (size_t)cdiv((int64_t)w.g.n_tiles * kPlanes * CT * 8, 256) * 256;
-  // segments of about sqrt(rows) rows: a segment's last tile and the channel tile's last tile
-  // each add about sqrt(rows) rows
-  const int64_t n_rows = B * (int64_t)w.g.n_chunks;
-  int64_t seg_rows = kMinSegRows;
-  while (seg_rows * seg_rows < n_rows) ++seg_rows;
-  w.seg_rows = (int)seg_rows;
-  w.n_seg = (int)cdiv(n_rows, seg_rows);
-  w.seg_off = w.part_off + (size_t)cdiv((int64_t)w.g.n_tiles * 3 * CT * 8, 256) * 256;
-  w.bytes = w.seg_off + (size_t)cdiv((int64_t)w.g.n_ctiles * w.n_seg * 3 * CT * 8, 256) * 256;
+  w.n_rows = (int)(B * (int64_t)w.g.n_chunks);
+  w.bytes = w.part_off + (size_t)cdiv((int64_t)w.g.n_tiles * 3 * CT * 4, 256) * 256;
   return w;
 }
 
@@ -2456,14 +2386,18 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
       grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
-      reinterpret_cast<uint64_t*>(ws + lay.part_off), reinterpret_cast<uint64_t*>(ws + lay.seg_off), \
-      lay.seg_rows, g.n_tiles, (uint32_t)n_chains, in_order)
+      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order)
   if (pf) {
     FL_BWK(true);
   } else {
     FL_BWK(false);
   }
 #undef FL_BWK
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return hip_status(e);
+  static_assert(CT == 64, "fl_param_grad_reduce_kernel sums rows of 64 channels");
+  fl_param_grad_reduce_kernel<<<(unsigned)(g.n_ctiles * 3), 1024, 0, stream>>>(
+      reinterpret_cast<const float*>(ws + lay.part_off), lay.n_rows, (int)C, grad_tr, grad_ti, grad_gamma);
   return hip_status(hipGetLastError());
 }
 

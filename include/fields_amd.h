@@ -148,9 +148,10 @@ int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, i
  *
  * Replaces `_ChunkedFieldReadFunction.backward`
  * (field_only_v4_chunked_triton_wiki100.py:1020-1105; Triton kernels 625-910: chunk summary,
- * chunk carry, chunk materialise, then a torch sum of the parameter partials). One launch: the
- * reverse scan (decoupled look-back over chunks taken in reverse time order), whose tiles also add
- * up the parameter gradients in a fixed order (bit-reproducible).
+ * chunk carry, chunk materialise, then a torch sum of the parameter partials). Two launches on
+ * `stream`: the reverse scan (decoupled look-back over chunks taken in reverse time order), whose
+ * tiles write per-tile parameter-gradient partials into the workspace, then a reduction that adds
+ * them up in a fixed order (bit-reproducible).
  *
  *   raw, strides, tr, ti, gamma, state_in   as given to the forward call
  *   read            [B, T, 4C] fp32, the forward output (the state planes at every 8th row

@@ -160,8 +160,8 @@ def test_backward_full_size_config2_row(dev):
 
 
 def test_backward_many_reduction_rows(dev):
-    """B=48, T=1500 (24 chunks, the last partial): 1,152 partial rows per channel tile, reduced in
-    34 segments of up to 34 rows. Batch rows are independent, so the parameter gradients equal the
+    """B=48, T=1500 (24 chunks, the last partial): 1,152 partial rows per channel tile, added up
+    by the reduction launch. Batch rows are independent, so the parameter gradients equal the
     sum of those of four calls on 12 rows each, and grad_raw equals theirs bit for bit (a tile's
     arithmetic does not depend on B); repeated calls give the same bits."""
     from fields_lm_amd import field_scan, field_scan_backward
@@ -333,9 +333,9 @@ def test_backward_repeated_calls_with_empty_waves(dev, dtype):
 
 def test_backward_workspace_reuse_across_shapes(dev):
     """One backward workspace (the per-stream cache), calls alternating shape: the parameter
-    gradients of every call equal those of the shape's first call bit for bit (the in-launch
-    reduction never sums a partial an earlier call or shape left in the workspace: its words carry
-    the launch's epoch)."""
+    gradients of every call equal those of the shape's first call bit for bit (every tile writes
+    its row of partials before the reduction launch reads it, so nothing an earlier call or shape
+    left in the workspace is summed)."""
     from fields_lm_amd import field_scan, field_scan_backward
 
     print("[case] backward workspace reuse", flush=True)
