@@ -180,9 +180,13 @@ def field_scan_backward(raw: torch.Tensor, transition_r: torch.Tensor, transitio
         if t is not None and t.shape != (batch, 2 * channels):
             raise ValueError(f"{name} must be [B, 2C]")
     grad_raw = torch.empty((batch, length, 3 * channels), device=dev, dtype=raw.dtype)
-    g_tr, g_ti, g_gm = (torch.zeros(channels, device=dev, dtype=torch.float32) for _ in range(3))
-    g_sin = torch.zeros((batch, 2 * channels), device=dev, dtype=torch.float32) if return_state_grad else None
-    if batch and length and channels:
+    work = bool(batch and length and channels)
+    # the kernels write every element of the parameter gradients and of grad_state_in; zeros only
+    # where there is nothing to scan
+    alloc = torch.empty if work else torch.zeros
+    g_tr, g_ti, g_gm = (alloc(channels, device=dev, dtype=torch.float32) for _ in range(3))
+    g_sin = alloc((batch, 2 * channels), device=dev, dtype=torch.float32) if return_state_grad else None
+    if work:
         ws_bytes = int(lib.fl_scan_backward_workspace_bytes(batch, length, channels))
         ws = nat.scan_workspace(dev, ws_bytes, "backward")
         nat.before_call(ws, "fl_scan_backward")

@@ -331,6 +331,42 @@ def test_backward_repeated_calls_with_empty_waves(dev, dtype):
     assert nat.workspace_error(nat.scan_workspace(dev, 0, "backward")) == 0
 
 
+def test_backward_in_hip_graph(dev):
+    """fl_scan_backward (the reverse scan and its reduction launch) captured in a HIP graph on a
+    stream whose workspace already exists: every replay, with eager work between replays and the
+    outputs overwritten with NaN before each, equals the eager call bit for bit (grad_raw, the
+    parameter gradients, grad_state_in), so a replay writes every element of every output."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    print("[case] backward hipGraph", flush=True)
+    B, T, C = 3, 700, 128
+    g = torch.Generator().manual_seed(91)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, 91))
+    sin = torch.randn(B, 2 * C, generator=g).to(dev)
+    read = field_scan(raw, tr, ti, gamma, state_in=sin)
+    gread = torch.randn(B, T, 4 * C, generator=g).to(dev)
+    gso = torch.randn(B, 2 * C, generator=g).to(dev)
+    kw = dict(state_in=sin, grad_state_out=gso, return_state_grad=True)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # the eager call also creates the stream's backward workspace
+        eager = [t.clone() for t in field_scan_backward(raw, tr, ti, gamma, read, gread, **kw)]
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=s):
+        out = field_scan_backward(raw, tr, ti, gamma, read, gread, **kw)
+    for rep in range(3):
+        for t in out:
+            t.fill_(float("nan"))
+        field_scan(raw, tr, ti, gamma)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        for x, y in zip(out, eager):
+            assert torch.equal(x, y), rep
+
+
 def test_backward_workspace_reuse_across_shapes(dev):
     """One backward workspace (the per-stream cache), calls alternating shape: the parameter
     gradients of every call equal those of the shape's first call bit for bit (every tile writes
