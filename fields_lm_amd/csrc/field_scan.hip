@@ -1349,7 +1349,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
 
 // ------------------------------------------------------------------------------------------
 // Backward scan (fl_scan_backward): the adjoint of the forward recurrence (canon:625-910,
-// 1020-1105), one launch, tiles taken in reverse time order.
+// 1020-1105), one scan launch with tiles taken in reverse time order, then the parameter-gradient
+// reduction launch.
 //
 // With U_t = dL/ds_t and D_t = dL/d disp_t (grad_read), the gradient reaching s_t from later
 // steps, c_t, obeys (a_t = (1 - v_t) lam, conj = complex conjugate)
@@ -2341,7 +2342,7 @@ size_t workspace_bytes(int64_t B, int64_t T, int64_t C) {
 
 // Backward tiling (K channels per lane, L steps per wave, W waves, OCC waves per SIMD) and its
 // workspace: [header 2 KiB][status: tiles x u32][data: tiles x 5 x CT x u64]
-// [partials: tiles x 3 x CT x u64][segment totals: channel tiles x segments x 3 x CT x u64]
+// [parameter-gradient partials: channel tiles x 3 planes x (n_chunks x B) rows x CT fp32]
 constexpr LookbackTiling kBwdTiling = {1, 8, 8, 4};
 
 struct BwdLayout {
