@@ -7,7 +7,8 @@ state_out against ``oracle.scan_f64`` (canon:392-416) at 1e-4 (bf16 read: the fp
 to nearest even, 1e-2). Every fifth case also runs the fused RMSNorm epilogue against
 ``rms_norm_f64`` at 1e-4, and every seventh the backward, on a row prefix of the case (at most 60k
 token-channels), against the float64 autograd oracle at 1e-4 (bf16 grad_raw, the rounded fp32
-value, at 1e-2). The draws are fixed by the seed, so a failure names a reproducible case.
+value, at 1e-2). Separate cases draw decode steps (24) and backward calls (16, some with long
+chains of counter tickets). The draws are fixed by the seed, so a failure names a reproducible case.
 """
 from __future__ import annotations
 
@@ -151,3 +152,59 @@ def test_random_decode_step_against_oracle(dev, i):
         assert oracle.rel_err(normed.float().cpu(), exp_norm) <= (1e-2 if out_bf16 else 1e-4), step
         assert oracle.rel_err(st_plain.cpu(), exp_state) <= 1e-4, step
         assert torch.equal(st_plain, st_norm), step  # the same state update in both kernels
+
+
+@pytest.mark.parametrize("i", range(16))
+def test_random_backward_against_oracle(dev, i):
+    """Random B (1..6), C (1..300, multiples of 64 every third case), T up to 70,000 // (B * C) with
+    every fourth case past 64 tiles of 64 steps (counter tickets), a padded raw row stride, raw
+    dtype, state_in and dL/dstate_out present or not: ``field_scan_backward`` against the float64
+    autograd oracle (canon:1020-1105) at 1e-4 (bf16 grad_raw: the rounded fp32 value, 1e-2),
+    parameter gradients and grad_state_in (of the zero state when state_in is absent) included."""
+    from fields_lm_amd import field_scan, field_scan_backward
+
+    rng = np.random.default_rng(7000 + i)
+    C = 64 * int(rng.integers(1, 5)) if i % 3 == 0 else int(rng.integers(1, 301))
+    B = int(rng.integers(1, 7))
+    if i % 4 == 1:
+        B, C = 1, int(rng.integers(1, 9))
+        T = int(rng.integers(64 * 64 + 1, 64 * 90))
+    else:
+        T = int(rng.integers(1, max(2, 70_000 // (B * C))))
+    pad = int(rng.choice([0, 8, int(rng.integers(1, 17))]))
+    raw_bf16, with_state, with_gso = (bool(rng.integers(0, 2)) for _ in range(3))
+    print(f"[case] backward fuzz {i}: B={B} T={T} C={C} pad={pad} raw_bf16={raw_bf16} "
+          f"state={with_state} gso={with_gso}", flush=True)
+    g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+    full = torch.randn(B, T, 3 * C + pad, generator=g) * 2
+    if raw_bf16:
+        full = full.to(torch.bfloat16)
+    raw_cpu = full[..., :3 * C].float()
+    rl, th = ref.init_radius_theta(C)
+    tr, ti, gamma = ref.transition_params(rl + 0.5 * torch.randn(C, generator=g),
+                                          th + 0.3 * torch.randn(C, generator=g))
+    sin = torch.randn(B, 2 * C, generator=g) if with_state else None
+    gso = torch.randn(B, 2 * C, generator=g) if with_gso else None
+    gread = torch.randn(B, T, 4 * C, generator=g)
+    raw = full.to(dev)[..., :3 * C]  # row stride 3C + pad
+    d = [t.to(dev) for t in (tr, ti, gamma)]
+    sin_d = None if sin is None else sin.to(dev)
+    read = field_scan(raw, *d, state_in=sin_d)
+    g_raw, g_tr, g_ti, g_gm, g_sin = field_scan_backward(
+        raw, *d, read, gread.to(dev), state_in=sin_d,
+        grad_state_out=None if gso is None else gso.to(dev), return_state_grad=True)
+    r = raw_cpu.double().requires_grad_()
+    p = [t.double().requires_grad_() for t in (tr, ti, gamma)]
+    # without state_in the scan starts from zero: the gradient reaching it is dL/d(zero state)
+    s0 = (sin if sin is not None else torch.zeros(B, 2 * C)).double().requires_grad_()
+    out64, st64 = oracle.scan_f64_autograd(r, *p, s0)
+    loss = (out64 * gread.double()).sum()
+    if gso is not None:
+        loss = loss + (st64 * gso.double()).sum()
+    loss.backward()
+    assert oracle.rel_err(g_raw.float().cpu(), r.grad) <= (1e-2 if raw_bf16 else 1e-4)
+    assert oracle.rel_err(g_tr.cpu(), p[0].grad) <= 1e-4
+    assert oracle.rel_err(g_ti.cpu(), p[1].grad) <= 1e-4
+    assert oracle.rel_err(g_gm.cpu(), p[2].grad) <= 1e-4
+    assert oracle.rel_err(g_sin.cpu(), s0.grad) <= 1e-4
+
