@@ -7,8 +7,8 @@ state_out against ``oracle.scan_f64`` (canon:392-416) at 1e-4 (bf16 read: the fp
 to nearest even, 1e-2). Every fifth case also runs the fused RMSNorm epilogue against
 ``rms_norm_f64`` at 1e-4, and every seventh the backward, on a row prefix of the case (at most 60k
 token-channels), against the float64 autograd oracle at 1e-4 (bf16 grad_raw, the rounded fp32
-value, at 1e-2). Separate cases draw decode steps (24) and backward calls (16, some with long
-chains of counter tickets). The draws are fixed by the seed, so a failure names a reproducible case.
+value, at 1e-2). Separate cases draw decode steps (24), backward calls (16, some with long
+chains of counter tickets) and RMSNorm-epilogue scans (12, up to 64 channel tiles of siblings). The draws are fixed by the seed, so a failure names a reproducible case.
 """
 from __future__ import annotations
 
@@ -207,4 +207,48 @@ def test_random_backward_against_oracle(dev, i):
     assert oracle.rel_err(g_ti.cpu(), p[1].grad) <= 1e-4
     assert oracle.rel_err(g_gm.cpu(), p[2].grad) <= 1e-4
     assert oracle.rel_err(g_sin.cpu(), s0.grad) <= 1e-4
+
+
+@pytest.mark.parametrize("i", range(12))
+def test_random_norm_epilogue_against_oracle(dev, i):
+    """The fused RMSNorm epilogue on random shapes with up to 64 channel tiles of siblings:
+    C from 1 to 4,096 (the epilogue's limit; multiples of 64 every other case, so the LDS-staged
+    path runs too), B 1..4, T up to 400,000 // (B * C) with every fourth case past 64 chunks
+    (counter tickets), a padded raw row stride, raw dtype, fp32 or bf16 output, state_in or none:
+    ``field_scan_norm`` against ``rms_norm_f64(scan_f64(...))`` (canon:300-309 on canon:392-416's
+    read) at 1e-4 (bf16 output: 1e-2), state_out against the oracle state at 1e-4."""
+    from fields_lm_amd import field_scan_norm
+
+    rng = np.random.default_rng(9000 + i)
+    C = 64 * int(rng.integers(1, 65)) if i % 2 == 0 else int(rng.integers(1, 4097))
+    B = int(rng.integers(1, 5))
+    if i % 4 == 3:  # counter tickets with sibling groups of up to 8 channel tiles
+        B, C = 1, 64 * int(rng.integers(1, 9)) - int(rng.integers(0, 2)) * int(rng.integers(1, 64))
+        T = int(rng.integers(128 * 64 + 1, 128 * 80))
+    else:
+        T = int(rng.integers(1, max(2, 400_000 // (B * C))))
+    pad = int(rng.choice([0, 8, int(rng.integers(1, 17))]))
+    raw_bf16, out_bf16, with_state = (bool(rng.integers(0, 2)) for _ in range(3))
+    eps = float(rng.choice([1e-6, 0.05]))
+    print(f"[case] norm fuzz {i}: B={B} T={T} C={C} pad={pad} raw_bf16={raw_bf16} "
+          f"out_bf16={out_bf16} state={with_state}", flush=True)
+    g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+    full = torch.randn(B, T, 3 * C + pad, generator=g) * 2
+    if raw_bf16:
+        full = full.to(torch.bfloat16)
+    raw_cpu = full[..., :3 * C].float()
+    rl, th = ref.init_radius_theta(C)
+    tr, ti, gamma = ref.transition_params(rl + 0.5 * torch.randn(C, generator=g),
+                                          th + 0.3 * torch.randn(C, generator=g))
+    sin = torch.randn(B, 2 * C, generator=g) if with_state else None
+    w = torch.rand(4 * C, generator=g) + 0.5
+    raw = full.to(dev)[..., :3 * C]  # row stride 3C + pad
+    d = [t.to(dev) for t in (tr, ti, gamma)]
+    out, st = field_scan_norm(raw, *d, w.to(dev), eps, state_in=None if sin is None else sin.to(dev),
+                              return_state=True,
+                              out_dtype=torch.bfloat16 if out_bf16 else torch.float32)
+    exp_read, exp_state = oracle.scan_f64(raw_cpu, tr, ti, gamma, sin)
+    exp = oracle.rms_norm_f64(exp_read, w, eps)
+    assert oracle.rel_err(out.float().cpu(), exp) <= (1e-2 if out_bf16 else 1e-4)
+    assert oracle.rel_err(st.cpu(), exp_state) <= 1e-4
 
