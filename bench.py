@@ -117,6 +117,37 @@ def measured_traffic(workload: str, variant: str = "read_fp32"):
 INFINITY_CACHE_BYTES = 256 * 2**20
 COLD_SET_BYTES = 1 << 30  # rotated buffer sets add up to at least this: 4x the Infinity Cache
 PREPARE_LAUNCHES = 100  # untimed launches before the warm-up steps of every timed loop
+START_DELAY_US = 200.0  # device time queued ahead of a timed loop's start event
+
+
+_DELAY_LIB = []
+
+
+def device_delay(stream, us: float = START_DELAY_US) -> bool:
+    """Queues ``us`` microseconds of device time on ``stream`` (``fl_bench_device_delay``: one
+    wave sleeping on the wall clock, which always ends); False when the bench library is absent.
+    Queued after the synchronize that opens a timed loop and before its start event, it keeps the
+    device from reaching the start event while the host is still enqueueing the first timed
+    launch. Otherwise that wait (tens of µs after a synchronize) lands inside the events: 20 steps
+    of the config-2 scan read ≈ 2 µs per step slower than 200 steps."""
+    import ctypes
+
+    if not _DELAY_LIB:
+        from fields_lm_amd.build import BENCH_LIB_PATH
+
+        lib = None
+        if BENCH_LIB_PATH.exists():
+            lib = ctypes.CDLL(str(BENCH_LIB_PATH))
+            lib.fl_bench_device_delay.restype = ctypes.c_int
+            lib.fl_bench_device_delay.argtypes = [ctypes.c_double, ctypes.c_void_p]
+        _DELAY_LIB.append(lib)
+    lib = _DELAY_LIB[0]
+    if lib is None:
+        return False
+    rc = lib.fl_bench_device_delay(float(us), ctypes.c_void_p(stream.cuda_stream))
+    if rc != 0:
+        raise RuntimeError(f"fl_bench_device_delay: error {rc}")
+    return True
 
 
 def time_plan(plans, steps: int, warmup: int):
@@ -125,7 +156,9 @@ def time_plan(plans, steps: int, warmup: int):
     ``plans`` is one plan or a list of plans over distinct buffer sets, launched in rotation
     (step i runs plans[i % n]); with sets adding up to more than the 256 MB Infinity Cache,
     every launch finds its inputs in HBM only (cold). The events sit on the launch stream,
-    inside the synchronize bracket that the wall clock spans."""
+    inside the synchronize bracket that the wall clock spans; a device delay (``device_delay``)
+    queued ahead of the start event keeps the host's first enqueue out of the events. The wall
+    clock includes that delay."""
     import torch
 
     plans = plans if isinstance(plans, (list, tuple)) else [plans]
@@ -141,6 +174,7 @@ def time_plan(plans, steps: int, warmup: int):
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    device_delay(stream)
     start.record(stream)
     for i in range(steps):
         plans[i % len(plans)].run(stream)
@@ -814,7 +848,10 @@ def main() -> int:
             "bytes_per_token": bpt, "parallelism": "single-gpu",
             "cache": f"cold: {n_sets} rotated buffer sets of {plan_set_bytes(plans[0]) / 1e6:.0f} MB",
             "clock": "HIP events on the launch stream around the timed steps (value, ms_per_step, "
-                     "achieved); wall_ms_per_step is the host clock around the same steps",
+                     "achieved); wall_ms_per_step is the host clock around the same steps, "
+                     f"including a {START_DELAY_US:.0f} us device delay queued ahead of the start "
+                     "event so that the host's first enqueue stays out of the events",
+            "start_delay": "queued" if _DELAY_LIB and _DELAY_LIB[0] is not None else "bench library absent",
             "wall_ms_per_step": wall_ms,
         },
         "roofline": {

@@ -10,6 +10,9 @@
 //                         values are the raw values widened (fp32) or copied (bf16)
 //   fl_bench_stream_copy  a streaming copy of the same bytes: 16-byte loads of `in_bytes`,
 //                         16-byte non-temporal stores of `out_bytes`, grid-stride
+//   fl_bench_device_delay one wave that sleeps until the constant-rate wall clock has advanced by a
+//                         given number of ticks, queued before a timed loop's start event so that
+//                         the host has its first launches queued when the device reaches it
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -91,6 +94,12 @@ __global__ __launch_bounds__(256) void stream_copy_kernel(const u32x4* __restric
   }
 }
 
+// returns once wall_clock64() has advanced by `ticks` (a monotonic constant-rate counter)
+__global__ __launch_bounds__(64) void delay_kernel(uint64_t ticks) {
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
 }  // namespace
 
 extern "C" {
@@ -122,6 +131,19 @@ int fl_bench_stream_copy(const void* src, void* dst, size_t in_bytes, size_t out
   if ((uintptr_t)src % 16 != 0 || (uintptr_t)dst % 16 != 0) return 1;
   stream_copy_kernel<<<2048, 256, 0, static_cast<hipStream_t>(stream)>>>(
       static_cast<const u32x4*>(src), static_cast<u32x4*>(dst), in_bytes / 16, out_bytes / 16);
+  return (int)hipGetLastError();
+}
+
+// Queues ~`us` microseconds of device time (one wave) on `stream`; at most 10 ms.
+int fl_bench_device_delay(double us, void* stream) {
+  if (!(us >= 0.0) || us > 10000.0) return 1;
+  int dev = 0, khz = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return (int)e;
+  if (khz <= 0) return 1;
+  const uint64_t ticks = (uint64_t)(us * (double)khz / 1000.0);
+  delay_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(ticks);
   return (int)hipGetLastError();
 }
 

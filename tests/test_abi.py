@@ -183,15 +183,20 @@ def test_wait_check_raises_on_error_word(monkeypatch):
 
 
 def test_bench_library_exports():
-    """bench.py's measurement library (copy kernels of the scan's access pattern) loads and
-    exports its two entry points; its argument checks refuse shapes outside the pattern."""
+    """bench.py's measurement library (copy kernels of the scan's access pattern, the device delay)
+    loads and exports its three entry points; its argument checks refuse shapes outside the
+    pattern and delays outside 0..10 ms."""
     from fields_lm_amd import build
 
     if not build.BENCH_LIB_PATH.exists():
         build.build_bench()
     blib = ctypes.CDLL(str(build.BENCH_LIB_PATH))
-    for name in ("fl_bench_tile_copy", "fl_bench_stream_copy"):
+    for name in ("fl_bench_tile_copy", "fl_bench_stream_copy", "fl_bench_device_delay"):
         assert hasattr(blib, name), name
+    blib.fl_bench_device_delay.restype = ctypes.c_int
+    blib.fl_bench_device_delay.argtypes = [ctypes.c_double, ctypes.c_void_p]
+    assert blib.fl_bench_device_delay(-1.0, None) == 1      # refused before any HIP call
+    assert blib.fl_bench_device_delay(20000.0, None) == 1   # beyond 10 ms
     blib.fl_bench_tile_copy.restype = ctypes.c_int
     blib.fl_bench_tile_copy.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 3 + \
         [ctypes.c_int, ctypes.c_void_p]
