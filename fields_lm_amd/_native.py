@@ -125,9 +125,9 @@ def stream_handle(device: torch.device) -> ctypes.c_void_p:
 ERROR_OFFSET = 128
 SPIN_LIMIT_OFFSET = 384
 HOST_ERROR_OFFSET = 392
-# Published words carry 30 bits of a launch epoch that every launch advances, so a workspace is
-# zero-filled again before 2^30 launches have run on it; the wrappers do it every 2^29 calls.
-REZERO_CALLS = 1 << 29
+# Published words carry 30 bits of a launch epoch that every launch advances; the launch that
+# brings those 30 bits back to zero has its last block zero-fill the buffer after the header, so
+# no caller (graph replays and the static-scratch entry included) has to re-zero a workspace.
 
 
 class _HostWords:
@@ -159,12 +159,10 @@ _host_words = _HostWords()
 
 class WorkspaceGuard:
     """Host side of one workspace: a pinned host word whose address sits in the header (the
-    kernels set it when a bounded wait gives up, so no device read is needed to see it) and the
-    count of calls since the workspace was zero-filled."""
+    kernels set it when a bounded wait gives up, so no device read is needed to see it)."""
 
     def __init__(self, ws: torch.Tensor):
         self.host_error = _host_words.take()
-        self.calls = 0
         self.arm(ws)
 
     def arm(self, ws: torch.Tensor) -> None:
@@ -173,18 +171,13 @@ class WorkspaceGuard:
 
     def before_call(self, ws: torch.Tensor, what: str) -> None:
         """Raise RuntimeError if an earlier call on this workspace had a wait give up (its outputs
-        hold NaN where a value was missing); re-zero the workspace when the epoch is due to wrap."""
+        hold NaN where a value was missing)."""
         if int(self.host_error[0]) != 0:
             self.host_error.zero_()
             ws[ERROR_OFFSET:ERROR_OFFSET + 4].zero_()
             raise RuntimeError(
                 f"{what}: an earlier call on this workspace had a look-back wait give up; the "
                 "outputs of that call are invalid (NaN where a carry or a partner value was missing)")
-        self.calls += 1
-        if self.calls >= REZERO_CALLS and not torch.cuda.is_current_stream_capturing():
-            ws.zero_()
-            self.arm(ws)
-            self.calls = 0
 
 
 # Guards by (device, address) of their workspace tensor; an entry leaves with its tensor, so a

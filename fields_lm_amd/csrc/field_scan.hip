@@ -875,12 +875,54 @@ __device__ __forceinline__ float poison() { return __builtin_nanf(""); }
 // Called once per block (one thread), after the block's last use of the workspace: the last
 // block of the launch re-arms the counter for the next launch (next epoch). Blocks that refused
 // a ticket count too, so a counter that was out of range is re-armed by the launch that saw it.
+__device__ __forceinline__ void rearm(LookbackHeader* hdr, uint32_t epoch) {
+  const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
+  __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// One thread's block end (a block that refused an out-of-range ticket): counts toward the
+// launch's end; the last block re-arms the counter for the next launch.
 __device__ __forceinline__ void finish_block(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch) {
   const unsigned int d = atomicAdd(&hdr->done, 1u);
-  if (d == n_tiles - 1) {
-    const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
-    __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (d == n_tiles - 1) rearm(hdr, epoch);
+}
+
+// The part of the caller's buffer after the header that holds published words (16-byte units, in
+// at most two pieces so that the backward's parameter-gradient partials, which its reduction
+// launch reads next, stay out of it).
+struct ClearSpan {
+  uint4* a;
+  size_t na;
+  uint4* b;
+  size_t nb;
+};
+constexpr uint32_t kEpochMask = 0x3fffffffu;  // bits of the epoch that published words carry
+
+// A tile block's end, called by every thread of the block: counts the block toward the launch's
+// end, and the launch's last block re-arms the counter for the next launch (next epoch).
+// Published words carry 30 bits of the epoch, so a word written 2^30 launches earlier would carry
+// the tag of the current one. When the next epoch's 30 bits wrap to 0, the last block therefore
+// zero-fills the whole span first: every word any earlier launch left in the buffer (at any
+// shape's layout) goes, before any launch of the new cycle reads it. The barrier ahead of the
+// count makes it count whole blocks: every wave of a counted block is past its last access to
+// published words, so when the last block clears, no wave of the launch still reads them.
+__device__ __forceinline__ void finish_launch(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch,
+                                              const ClearSpan& clr) {
+  __shared__ int s_wrap;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned int d = atomicAdd(&hdr->done, 1u);
+    const bool last = d == n_tiles - 1;
+    const bool wrap = last && ((epoch + 1u) & kEpochMask) == 0u;
+    if (last && !wrap) rearm(hdr, epoch);
+    s_wrap = wrap ? 1 : 0;
+  }
+  __syncthreads();
+  if (s_wrap) {  // block-uniform
+    for (size_t i = threadIdx.x; i < clr.na; i += blockDim.x) clr.a[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (size_t i = threadIdx.x; i < clr.nb; i += blockDim.x) clr.b[i] = make_uint4(0u, 0u, 0u, 0u);
+    __syncthreads();
+    if (threadIdx.x == 0) rearm(hdr, epoch);
   }
 }
 constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
@@ -1084,7 +1126,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
     uint32_t* status, uint64_t* data, uint32_t n_tiles, bool in_order,
-    const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib) {
+    const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib, ClearSpan wrap_clear) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1344,7 +1386,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
   }
 
   // the last block of the launch re-arms the counter for the next launch (next epoch)
-  if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
+  finish_launch(hdr, n_tiles, epoch, wrap_clear);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1384,7 +1426,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
     float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
-    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order) {
+    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order, ClearSpan wrap_clear) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1752,7 +1794,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
   }
 
   // the last block of the launch re-arms the counter for the next launch (next epoch)
-  if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
+  finish_launch(hdr, n_tiles, epoch, wrap_clear);
 }
 
 // Parameter gradients (dlam = grad_tr + i grad_ti and dgamma, summed over batch rows and steps):
@@ -2232,19 +2274,28 @@ struct NormArgs {
 };
 
 // Where a launch keeps its look-back state: the header, the status words, the tagged data words
-// and (RMSNorm epilogue) the per-row partials.
+// and (RMSNorm epilogue) the per-row partials; and the span cleared when the epoch wraps.
 struct WsRegions {
   LookbackHeader* hdr;
   uint32_t* status;
   uint64_t* data;
   uint64_t* sib;
+  ClearSpan clr;
 };
 
-WsRegions regions_of(void* workspace, int64_t B, int64_t T, int64_t C) {
+// The whole buffer after the header (`bytes` as the caller gave it), in 16-byte units.
+ClearSpan clear_span_after_header(void* buffer, size_t bytes) {
+  char* p = static_cast<char*>(buffer) + kHeaderBytes;
+  const size_t n = bytes > kHeaderBytes ? (bytes - kHeaderBytes) / 16 : 0;
+  return {reinterpret_cast<uint4*>(p), n, nullptr, 0};
+}
+
+WsRegions regions_of(void* workspace, size_t workspace_bytes_given, int64_t B, int64_t T, int64_t C) {
   const WorkspaceLayout lay = workspace_layout(B, T, C);
   char* ws = static_cast<char*>(workspace);
   return {reinterpret_cast<LookbackHeader*>(ws), reinterpret_cast<uint32_t*>(ws + lay.status_off),
-          reinterpret_cast<uint64_t*>(ws + lay.data_off), reinterpret_cast<uint64_t*>(ws + lay.sib_off)};
+          reinterpret_cast<uint64_t*>(ws + lay.data_off), reinterpret_cast<uint64_t*>(ws + lay.sib_off),
+          clear_span_after_header(workspace, workspace_bytes_given)};
 }
 
 template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
@@ -2266,7 +2317,7 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
-      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib);
+      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, rg.clr);
   return hip_status(hipGetLastError());
 }
 
@@ -2368,12 +2419,20 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
                     const float* read, const float* grad_read, const float* grad_state_out,
                     void* grad_raw, float* grad_tr, float* grad_ti, float* grad_gamma,
-                    float* grad_state_in, void* workspace, hipStream_t stream) {
+                    float* grad_state_in, void* workspace, size_t workspace_bytes_given,
+                    hipStream_t stream) {
   constexpr LookbackTiling tl = kBwdTiling;
   constexpr int CT = 64 * tl.k;
   const BwdLayout lay = bwd_layout(B, T, C);
   const LookbackGeom& g = lay.g;
   char* ws = static_cast<char*>(workspace);
+  // cleared when the epoch wraps: the buffer after the header, except this call's partials,
+  // which the reduction launch reads after the scan (every tile writes its row of them, which
+  // overwrites whatever an earlier launch left there)
+  const size_t part_end = lay.part_off + (size_t)cdiv((int64_t)g.n_tiles * 3 * CT * 4, 16) * 16;
+  ClearSpan clr{reinterpret_cast<uint4*>(ws + kHeaderBytes), (lay.part_off - kHeaderBytes) / 16,
+                reinterpret_cast<uint4*>(ws + part_end),
+                workspace_bytes_given > part_end ? (workspace_bytes_given - part_end) / 16 : 0};
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
   // ticket order as in the forward launch: block order for short chains, one counter otherwise
   const bool in_order = g.n_chunks <= 64;
@@ -2387,7 +2446,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
       grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
-      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order)
+      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order, clr)
   if (pf) {
     FL_BWK(true);
   } else {
@@ -2460,7 +2519,7 @@ int scan_impl(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool raw16 = raw_dtype == FL_DTYPE_BF16, out16 = read_dtype == FL_DTYPE_BF16;
-  const WsRegions rg = fixed != nullptr ? *fixed : regions_of(workspace, B, T, C);
+  const WsRegions rg = fixed != nullptr ? *fixed : regions_of(workspace, workspace_bytes_given, B, T, C);
   if (base_algo == FL_ALGO_CHUNKED3) {
     const int64_t n_chunks = cdiv(T, kChunkT);
     float* agg = reinterpret_cast<float*>(static_cast<char*>(workspace) +
@@ -2627,7 +2686,8 @@ int fl_scan_forward_static(const void* raw, int raw_dtype, int64_t B, int64_t T,
   if (rc != FL_OK) return rc;
   const WsRegions rg{reinterpret_cast<LookbackHeader*>(base),
                      reinterpret_cast<uint32_t*>(base + kStaticStatusOff),
-                     reinterpret_cast<uint64_t*>(base + kStaticDataOff), nullptr};
+                     reinterpret_cast<uint64_t*>(base + kStaticDataOff), nullptr,
+                     clear_span_after_header(base, kStaticScratchBytes)};
   return scan_impl(raw, raw_dtype, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in,
                    state_out, read, read_dtype, nullptr, 0, FL_ALGO_AUTO, NormArgs{nullptr, 0.f},
                    stream, &rg);
@@ -2727,7 +2787,7 @@ int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64
 #define FL_BW(R, G)                                                                              \
   return launch_backward<R, G>(raw, B, T, C, raw_stride_b, raw_stride_t, tr, ti, gamma, state_in, \
                                read, grad_read, grad_state_out, grad_raw, grad_tr, grad_ti,       \
-                               grad_gamma, grad_state_in, workspace, s);
+                               grad_gamma, grad_state_in, workspace, workspace_bytes_given, s);
   const bool raw16 = raw_dtype == FL_DTYPE_BF16, g16 = grad_raw_dtype == FL_DTYPE_BF16;
   if (raw16 && g16) { FL_BW(bf16_bits, bf16_bits) }
   if (raw16) { FL_BW(bf16_bits, float) }

@@ -74,7 +74,8 @@ extern "C" {
  *              aligned, ZERO-FILLED before its first use and then reused as is: its first 2 KiB
  *              hold launch counters that every call leaves ready for the next one. Calls on one
  *              workspace must be stream-ordered (one workspace per stream). Every launch advances
- *              a 30-bit epoch kept there: zero-fill the workspace again before 2^30 launches.
+ *              an epoch kept there; the launch at each 2^30-launch wrap of its tag bits zero-fills
+ *              the rest of the workspace itself, so it is never zero-filled again by the caller.
  *
  * Workspace header (first 2 KiB; little-endian words at these byte offsets):
  *   128  u32  error word: bit 0 a bounded wait gave up, bit 1 a ticket beyond the launch's tiles

@@ -163,7 +163,7 @@ def test_workspace_at_a_reused_address_has_its_own_guard(dev, monkeypatch):
     ws = plan.workspace
     guard = nat._guards[(dev.index, ws.data_ptr())]
     named = int(ws[392:400].cpu().view(torch.int64).item())
-    assert named == guard.host_error.data_ptr() and guard.calls == 0
+    assert named == guard.host_error.data_ptr()
     print(f"[case] same address as the freed plan: {ws.data_ptr() == first}", flush=True)
     _seed_counter(ws, epoch=3, first_ticket=66 - 1)
     nat.set_spin_limit(ws, 16)
@@ -176,3 +176,67 @@ def test_workspace_at_a_reused_address_has_its_own_guard(dev, monkeypatch):
     torch.cuda.synchronize()
     exp, _ = oracle.scan_f64(raw.float().cpu(), tr.cpu(), ti.cpu(), gamma.cpu())
     assert oracle.rel_err(out.cpu(), exp) <= 1e-4
+
+
+def _plant_stale_words(ws):
+    """Every 32-bit word after the header set to 2: a status word saying "inclusive state
+    published" and data words carrying that tag, for the first epoch after the 30-bit wrap. They
+    stand for words left 2^30 launches earlier, with a carry of ~0 that no correct scan has."""
+    ws[2048:].view(torch.int32).fill_(2)
+
+
+def _inputs(B, T, C, seed):
+    g = torch.Generator().manual_seed(seed)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16)
+    tr, ti, gamma = _params(C, seed=seed + 1)
+    return raw, tr, ti, gamma, torch.rand(4 * C, generator=g) + 0.5, torch.randn(B, T, 4 * C, generator=g)
+
+
+# the wrap launch runs a small shape; the launch after it a larger one, whose look-back reads
+# status and data words the small launch never wrote (planted with the new cycle's tags)
+SMALL, LARGE = (1, 256, 64), (2, 1000, 128)
+
+
+@pytest.mark.parametrize("kind", ["plain", "norm", "backward"])
+def test_epoch_wrap_clears_published_words(dev, kind):
+    """The launch that advances the epoch to 2^30 (whose 30 tag bits are 0) zero-fills the
+    workspace after its header, so that no word left from 2^30 launches earlier can pass for one
+    of the new cycle. Stale words carrying the new cycle's tags are planted in the whole buffer,
+    the epoch is set to 2^30 - 1, and a small shape runs (the wrap launch); a larger shape then
+    reads planted words the small one never rewrote. Both are bit-identical to ordinary calls. For
+    the forward workspace everything after the header is zero between the two calls. The backward
+    keeps the wrap launch's parameter-gradient partials, which its reduction launch reads."""
+    from fields_lm_amd import _native as nat
+    from fields_lm_amd import field_scan, field_scan_backward, field_scan_norm
+
+    print(f"[case] epoch wrap {kind}", flush=True)
+    data = {shape: [t.to(dev) for t in _inputs(*shape, seed=81 + shape[2])] for shape in (SMALL, LARGE)}
+
+    def call(shape):
+        raw, tr, ti, gamma, weight, gread = data[shape]
+        if kind == "norm":
+            return [field_scan_norm(raw, tr, ti, gamma, weight, 1e-6, out_dtype=torch.bfloat16)]
+        if kind == "plain":
+            return [field_scan(raw, tr, ti, gamma)]
+        read = field_scan(raw, tr, ti, gamma)
+        return list(field_scan_backward(raw, tr, ti, gamma, read, gread))
+
+    ref_large = [t.clone() for t in call(LARGE)]  # also sizes the stream's workspace for LARGE
+    ref_small = [t.clone() for t in call(SMALL)]
+    torch.cuda.synchronize()
+    ws = nat.scan_workspace(dev, 0, "backward" if kind == "backward" else "forward")
+    _plant_stale_words(ws)
+    _seed_counter(ws, epoch=(1 << 30) - 1, first_ticket=0)
+    wrap_small = call(SMALL)
+    torch.cuda.synchronize()
+    for x, y in zip(wrap_small, ref_small):
+        assert torch.equal(x, y)
+    epoch = int(ws[TICKET_OFFSET:TICKET_OFFSET + 8].view(torch.int64).item()) >> 32
+    assert epoch == 1 << 30
+    if kind != "backward":
+        assert int(ws[2048:].count_nonzero()) == 0
+    after_large = call(LARGE)
+    torch.cuda.synchronize()
+    for x, y in zip(after_large, ref_large):
+        assert torch.equal(x, y)
+    assert nat.workspace_error(ws) == 0
