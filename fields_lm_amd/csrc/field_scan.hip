@@ -872,16 +872,13 @@ __device__ __forceinline__ void report_error(LookbackHeader* hdr, uint32_t bits)
 
 __device__ __forceinline__ float poison() { return __builtin_nanf(""); }
 
-// Called once per block (one thread), after the block's last use of the workspace: the last
-// block of the launch re-arms the counter for the next launch (next epoch). Blocks that refused
-// a ticket count too, so a counter that was out of range is re-armed by the launch that saw it.
+// The counter armed for the next launch (next epoch), by the launch's last block.
 __device__ __forceinline__ void rearm(LookbackHeader* hdr, uint32_t epoch) {
   const unsigned long long armed = (unsigned long long)(epoch + 1u) << 32;
   __hip_atomic_store(&hdr->ticket, armed, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// One thread's block end (a block that refused an out-of-range ticket): counts toward the
-// launch's end; the last block re-arms the counter for the next launch.
+// One thread's count of its block toward the launch's end; the last block re-arms the counter.
 __device__ __forceinline__ void finish_block(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch) {
   const unsigned int d = atomicAdd(&hdr->done, 1u);
   if (d == n_tiles - 1) rearm(hdr, epoch);
@@ -898,27 +895,33 @@ struct ClearSpan {
 };
 constexpr uint32_t kEpochMask = 0x3fffffffu;  // bits of the epoch that published words carry
 
-// A tile block's end, called by every thread of the block: counts the block toward the launch's
-// end, and the launch's last block re-arms the counter for the next launch (next epoch).
+// A block's end, called by every thread of the block: counts the block toward the launch's end,
+// and the launch's last block re-arms the counter for the next launch (next epoch). Blocks that
+// refused a ticket count too, so a counter that was out of range is re-armed by the launch that
+// saw it.
 // Published words carry 30 bits of the epoch, so a word written 2^30 launches earlier would carry
-// the tag of the current one. When the next epoch's 30 bits wrap to 0, the last block therefore
-// zero-fills the whole span first: every word any earlier launch left in the buffer (at any
-// shape's layout) goes, before any launch of the new cycle reads it. The barrier ahead of the
-// count makes it count whole blocks: every wave of a counted block is past its last access to
-// published words, so when the last block clears, no wave of the launch still reads them.
+// the tag of the current one. In the launch whose next epoch's 30 bits wrap to 0 (the same epoch,
+// so the same branch, for every block), the last block therefore zero-fills the whole span first:
+// every word any earlier launch left in the buffer (at any shape's layout) goes, before any launch
+// of the new cycle reads it. There every block counts only after a barrier (all its waves are past
+// their last access to published words) and with release-acquire ordering, so the clear lands
+// after every store of the launch and no wave still reads what it clears. Every other launch
+// counts with one thread and no barrier.
 __device__ __forceinline__ void finish_launch(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch,
                                               const ClearSpan& clr) {
-  __shared__ int s_wrap;
+  if (((epoch + 1u) & kEpochMask) != 0u) {
+    if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
+    return;
+  }
+  __shared__ int s_last;
   __syncthreads();
   if (threadIdx.x == 0) {
-    const unsigned int d = atomicAdd(&hdr->done, 1u);
-    const bool last = d == n_tiles - 1;
-    const bool wrap = last && ((epoch + 1u) & kEpochMask) == 0u;
-    if (last && !wrap) rearm(hdr, epoch);
-    s_wrap = wrap ? 1 : 0;
+    const unsigned int d =
+        __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = d == n_tiles - 1 ? 1 : 0;
   }
   __syncthreads();
-  if (s_wrap) {  // block-uniform
+  if (s_last) {  // block-uniform
     for (size_t i = threadIdx.x; i < clr.na; i += blockDim.x) clr.a[i] = make_uint4(0u, 0u, 0u, 0u);
     for (size_t i = threadIdx.x; i < clr.nb; i += blockDim.x) clr.b[i] = make_uint4(0u, 0u, 0u, 0u);
     __syncthreads();
@@ -1169,10 +1172,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
     if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
-      if (threadIdx.x == 0) {
-        report_error(hdr, 2u);
-        finish_block(hdr, n_tiles, s_tk[1]);
-      }
+      if (threadIdx.x == 0) report_error(hdr, 2u);
+      finish_launch(hdr, n_tiles, (uint32_t)uniform((int)s_tk[1]), wrap_clear);
       return;
     }
   }
@@ -1462,10 +1463,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
     if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
-      if (threadIdx.x == 0) {
-        report_error(hdr, 2u);
-        finish_block(hdr, n_tiles, s_tk[1]);
-      }
+      if (threadIdx.x == 0) report_error(hdr, 2u);
+      finish_launch(hdr, n_tiles, (uint32_t)uniform((int)s_tk[1]), wrap_clear);
       return;
     }
   }
