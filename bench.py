@@ -549,7 +549,7 @@ def backward_timing(workload: str, steps: int = 50, warmup: int = 5, cold_only: 
             "frac_hbm_peak": nbytes / (ev * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "hot_us_per_step": hot * 1e3, "hot_frac_hbm_peak": nbytes / (hot * 1e-3) / 1e9 / HBM_PEAK_GBS,
             "cache": f"cold: {n_sets} rotated buffer sets; hot: one set replayed",
-            "note": "one launch: the reverse scan and the parameter-gradient reduction"}
+            "note": "two launches: the reverse scan, then the parameter-gradient reduction"}
 
 
 def _promoted_model(dev):

@@ -879,6 +879,8 @@ __device__ __forceinline__ void rearm(LookbackHeader* hdr, uint32_t epoch) {
   __hip_atomic_store(&hdr->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // One thread's count of its block toward the launch's end; the last block re-arms the counter.
+// Blocks that refused an out-of-range ticket count too, so a counter that was out of range is
+// re-armed by the launch that saw it.
 __device__ __forceinline__ void finish_block(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch) {
   const unsigned int d = atomicAdd(&hdr->done, 1u);
   if (d == n_tiles - 1) rearm(hdr, epoch);
@@ -895,37 +897,34 @@ struct ClearSpan {
 };
 constexpr uint32_t kEpochMask = 0x3fffffffu;  // bits of the epoch that published words carry
 
-// A block's end, called by every thread of the block: counts the block toward the launch's end,
-// and the launch's last block re-arms the counter for the next launch (next epoch). Blocks that
-// refused a ticket count too, so a counter that was out of range is re-armed by the launch that
-// saw it.
+// A forward tile block's end, called by every thread of the block: counts the block toward the
+// launch's end, and the launch's last block re-arms the counter for the next launch (next epoch).
 // Published words carry 30 bits of the epoch, so a word written 2^30 launches earlier would carry
 // the tag of the current one. In the launch whose next epoch's 30 bits wrap to 0 (the same epoch,
-// so the same branch, for every block), the last block therefore zero-fills the whole span first:
-// every word any earlier launch left in the buffer (at any shape's layout) goes, before any launch
-// of the new cycle reads it. There every block counts only after a barrier (all its waves are past
-// their last access to published words) and with release-acquire ordering, so the clear lands
-// after every store of the launch and no wave still reads what it clears. Every other launch
-// counts with one thread and no barrier.
+// so the same branch, for every block), the last block therefore zero-fills the whole span first
+// (one thread: a few ms, once in 2^30 launches): every word any earlier launch left in the buffer
+// (at any shape's layout) goes, before any launch of the new cycle reads it. There every block
+// counts only after a barrier (all its waves are past their last access to published words) and
+// with release-acquire ordering, so the clear lands after every store of the launch and no wave
+// still reads what it clears. Every other launch counts with one thread and no barrier. (Code
+// here is in the kernel's tail; written this way it leaves the generated code of the kernel's
+// body as it is without it.) A block that refused an out-of-range ticket counts through
+// finish_block and never clears: such a launch has already set the error word.
 __device__ __forceinline__ void finish_launch(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch,
                                               const ClearSpan& clr) {
-  if (((epoch + 1u) & kEpochMask) != 0u) {
-    if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
-    return;
-  }
-  __shared__ int s_last;
-  __syncthreads();
+  const bool wrap = ((epoch + 1u) & kEpochMask) == 0u;
+  if (wrap) __syncthreads();
   if (threadIdx.x == 0) {
     const unsigned int d =
-        __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = d == n_tiles - 1 ? 1 : 0;
-  }
-  __syncthreads();
-  if (s_last) {  // block-uniform
-    for (size_t i = threadIdx.x; i < clr.na; i += blockDim.x) clr.a[i] = make_uint4(0u, 0u, 0u, 0u);
-    for (size_t i = threadIdx.x; i < clr.nb; i += blockDim.x) clr.b[i] = make_uint4(0u, 0u, 0u, 0u);
-    __syncthreads();
-    if (threadIdx.x == 0) rearm(hdr, epoch);
+        wrap ? __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT)
+             : atomicAdd(&hdr->done, 1u);
+    if (d == n_tiles - 1) {
+      if (wrap) {
+        for (size_t i = 0; i < clr.na; ++i) clr.a[i] = make_uint4(0u, 0u, 0u, 0u);
+        for (size_t i = 0; i < clr.nb; ++i) clr.b[i] = make_uint4(0u, 0u, 0u, 0u);
+      }
+      rearm(hdr, epoch);
+    }
   }
 }
 constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
@@ -1172,8 +1171,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
     if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
-      if (threadIdx.x == 0) report_error(hdr, 2u);
-      finish_launch(hdr, n_tiles, (uint32_t)uniform((int)s_tk[1]), wrap_clear);
+      if (threadIdx.x == 0) {
+        report_error(hdr, 2u);
+        finish_block(hdr, n_tiles, s_tk[1]);
+      }
       return;
     }
   }
@@ -1427,7 +1428,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
     float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
-    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order, ClearSpan wrap_clear) {
+    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order) {
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1463,8 +1464,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
     if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
-      if (threadIdx.x == 0) report_error(hdr, 2u);
-      finish_launch(hdr, n_tiles, (uint32_t)uniform((int)s_tk[1]), wrap_clear);
+      if (threadIdx.x == 0) {
+        report_error(hdr, 2u);
+        finish_block(hdr, n_tiles, s_tk[1]);
+      }
       return;
     }
   }
@@ -1792,8 +1795,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     }
   }
 
-  // the last block of the launch re-arms the counter for the next launch (next epoch)
-  finish_launch(hdr, n_tiles, epoch, wrap_clear);
+  // the last block of the launch re-arms the counter for the next launch (next epoch); the
+  // reduction launch clears the workspace when that epoch wraps the published words' tags
+  if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
 }
 
 // Parameter gradients (dlam = grad_tr + i grad_ti and dgamma, summed over batch rows and steps):
@@ -1801,11 +1805,18 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
 // 2: dgamma) added up over the n_rows rows of each channel tile. One block per (channel tile,
 // plane), lane = channel: wave w adds its run of rows in order, then wave 0 adds the 16 wave sums
 // in order, so the sums do not depend on timing.
+// It also keeps the backward workspace's published words valid across the epoch's wrap: it runs
+// after the scan launch has ended, and when the epoch that launch armed for the next one has the
+// low 30 bits 0 (the tags of a new cycle), its blocks zero-fill `wrap_clear` (the workspace after
+// the header, less the partials) between them, so that no word left 2^30 launches earlier can
+// pass for one of the new cycle. The scan launch itself then needs no code for it.
 __global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float* __restrict__ part,
                                                                    int n_rows, int C,
                                                                    float* __restrict__ grad_tr,
                                                                    float* __restrict__ grad_ti,
-                                                                   float* __restrict__ grad_gamma) {
+                                                                   float* __restrict__ grad_gamma,
+                                                                   const LookbackHeader* hdr,
+                                                                   ClearSpan wrap_clear) {
   constexpr int CT = 64, NW = 16, kBatch = 32;
   __shared__ float s_acc[NW][CT];
   const int lane = threadIdx.x & 63;
@@ -1830,6 +1841,16 @@ __global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float*
     for (int u = 0; u < NW; ++u) t += s_acc[u][lane];
     const int c = ctile * CT + lane;
     if (c < C) (plane == 0 ? grad_tr : plane == 1 ? grad_ti : grad_gamma)[c] = t;
+  }
+  const uint32_t next_epoch = (uint32_t)(__hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT) >> 32);
+  if ((next_epoch & kEpochMask) == 0u) {  // uniform over the grid
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < wrap_clear.na; i += stride)
+      wrap_clear.a[i] = z;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < wrap_clear.nb; i += stride)
+      wrap_clear.b[i] = z;
   }
 }
 
@@ -2425,8 +2446,8 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const BwdLayout lay = bwd_layout(B, T, C);
   const LookbackGeom& g = lay.g;
   char* ws = static_cast<char*>(workspace);
-  // cleared when the epoch wraps: the buffer after the header, except this call's partials,
-  // which the reduction launch reads after the scan (every tile writes its row of them, which
+  // cleared by the reduction launch when the epoch wraps: the buffer after the header, except
+  // this call's partials, which that launch reads (every tile writes its row of them, which
   // overwrites whatever an earlier launch left there)
   const size_t part_end = lay.part_off + (size_t)cdiv((int64_t)g.n_tiles * 3 * CT * 4, 16) * 16;
   ClearSpan clr{reinterpret_cast<uint4*>(ws + kHeaderBytes), (lay.part_off - kHeaderBytes) / 16,
@@ -2445,7 +2466,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
       grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
-      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order, clr)
+      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order)
   if (pf) {
     FL_BWK(true);
   } else {
@@ -2456,7 +2477,8 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   if (e != hipSuccess) return hip_status(e);
   static_assert(CT == 64, "fl_param_grad_reduce_kernel sums rows of 64 channels");
   fl_param_grad_reduce_kernel<<<(unsigned)(g.n_ctiles * 3), 1024, 0, stream>>>(
-      reinterpret_cast<const float*>(ws + lay.part_off), lay.n_rows, (int)C, grad_tr, grad_ti, grad_gamma);
+      reinterpret_cast<const float*>(ws + lay.part_off), lay.n_rows, (int)C, grad_tr, grad_ti, grad_gamma,
+      reinterpret_cast<const LookbackHeader*>(ws), clr);
   return hip_status(hipGetLastError());
 }
 
