@@ -234,7 +234,11 @@ class LandmarkAttention(nn.Module):
     def new_state(self, batch: int, max_len: int, device, dtype) -> Dict[str, torch.Tensor]:
         self._rope_len = int(max_len)
         hd, h, w = self.head_dim, self.kv_heads, self.local_window
-        n_land = max_len // self.landmark_chunk
+        # landmark slots: 0 is the null slot, slot k + 1 holds chunk k's landmark. The step at
+        # position p writes its own chunk's running landmark to slot p // c + 1, so positions
+        # below max_len use slots up to (max_len - 1) // c + 1 (with fewer, the last chunk's
+        # running landmark would land on the one before it, which later tokens read)
+        n_land = (max_len - 1) // self.landmark_chunk + 1
         return {
             "kt": torch.zeros(batch, h, hd, w, device=device, dtype=dtype),   # keys, transposed
             "v": torch.zeros(batch, h, w, hd, device=device, dtype=dtype),
@@ -316,6 +320,7 @@ class LandmarkAttention(nn.Module):
         mean = (st["lat_sum"] / c).to(x_t.dtype)
         lk, lv = self.kv_up(mean).split(hkv * hd, dim=-1)
         lk = apply_rope(lk.view(b, hkv, hd), ct, stt)
+        # (the clamp only keeps a position past max_len, which is not supported, in bounds)
         lslot = torch.clamp(chunk + 1, max=n_slots - 1).view(1)
         st["lkt"].index_copy_(3, lslot, lk.unsqueeze(-1))
         st["lv"].index_copy_(2, lslot, lv.view(b, hkv, 1, hd))

@@ -89,6 +89,22 @@ def test_landmark_attention_decode_equals_forward(prompt):
     torch.testing.assert_close(torch.stack(steps, 1), full[:, prompt:], rtol=1e-4, atol=1e-5)
 
 
+@pytest.mark.parametrize("max_len", [20, 21, 22, 23, 24, 25])
+def test_landmark_attention_decode_to_max_len(max_len):
+    """Decoding to the last position the state is sized for (max_len - 1), for max_len on and a
+    few tokens past a chunk boundary. Each step writes its own chunk's running landmark to the
+    slot after the completed chunks', so the state needs that slot too: with one slot too few the
+    write landed on the previous chunk's landmark, which every later token of the chunk reads."""
+    a = _attn()
+    x = torch.randn(2, max_len, 64)
+    with torch.no_grad():
+        full = a(x)
+        y, st = a.prefill(x[:, :5], max_len=max_len)
+        steps = [a.step(x[:, t], torch.tensor(t), st) for t in range(5, max_len)]
+    torch.testing.assert_close(y, full[:, :5], rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(torch.stack(steps, 1), full[:, 5:], rtol=1e-4, atol=1e-5)
+
+
 def test_refresh_block_decode_equals_forward():
     torch.manual_seed(6)
     blk = M.RefreshBlock(64, 4, 2, 16, 8, 4, 96)
