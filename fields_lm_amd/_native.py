@@ -171,13 +171,15 @@ class WorkspaceGuard:
 
     def before_call(self, ws: torch.Tensor, what: str) -> None:
         """Raise RuntimeError if an earlier call on this workspace had a wait give up (its outputs
-        hold NaN where a value was missing)."""
+        hold NaN where a value was missing) or blocks that found the ticket counter out of range
+        (their tiles were not computed; the parameter gradients of a backward are NaN)."""
         if int(self.host_error[0]) != 0:
             self.host_error.zero_()
             ws[ERROR_OFFSET:ERROR_OFFSET + 4].zero_()
             raise RuntimeError(
-                f"{what}: an earlier call on this workspace had a look-back wait give up; the "
-                "outputs of that call are invalid (NaN where a carry or a partner value was missing)")
+                f"{what}: an earlier call on this workspace had a look-back wait give up or a "
+                "ticket out of range; the outputs of that call are invalid (NaN where a carry or a "
+                "partner value was missing, not written where a tile was refused)")
 
 
 # Guards by (device, address) of their workspace tensor; an entry leaves with its tensor, so a

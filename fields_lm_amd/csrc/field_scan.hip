@@ -350,71 +350,155 @@ struct WaveTile {
     }
   }
 
-  // materialize() (NORM: materialize_norm()) through a per-wave LDS region `stage` (4 planes x
-  // R rows x 64 floats): each group of R rows is written to LDS one channel per lane, read back
-  // as 16 bytes of output per lane (4 fp32 or 8 bf16 channels of one row-plane) and stored with
-  // 16-byte buffer stores. The whole store offset is in voffset, so rows past the descriptor's
-  // bound (past T) are dropped by it; the tile's 64 channels must all lie below C.
+  // One step from (sr, si) with row j's gates: m = lam * s_prev, disp = v * m = m - keep * m,
+  // s = keep * m + b (canon:583-621). The complex product goes through cmul, so that every pass
+  // (plain stores, LDS-staged stores, the RMSNorm epilogue's value pass) rounds alike.
+  __device__ __forceinline__ void step(int j, int k, float lr, float li, float& sr, float& si,
+                                       float& dr, float& di) const {
+    float mr, mi;
+    cmul(lr, li, sr, si, mr, mi);
+    dr = fmaf(-gk[j][k], mr, mr);
+    di = fmaf(-gk[j][k], mi, mi);
+    sr = fmaf(gk[j][k], mr, gbr[j][k]);
+    si = fmaf(gk[j][k], mi, gbi[j][k]);
+  }
+
+  // Stores of a per-wave LDS region `stage` (4 planes x R rows x 64 floats, written one channel
+  // per lane): read back as 16 bytes of output per lane (4 fp32 or 8 bf16 channels of one
+  // row-plane) and stored with 16-byte buffer stores at byte offset off0 + row * row_bytes +
+  // plane * plane_bytes + 16 * piece. The whole offset is in voffset, so rows past the
+  // descriptor's bound (past T) are dropped by it.
+  template <typename OutT, int R>
+  __device__ __forceinline__ static void store_stage(rsrc_t w, int lane, int off0, int row_bytes,
+                                                     int plane_bytes, const float* stage) {
+    // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
+    // the compiler's wait states for a VALU op overwriting the store's data VGPRs right after
+    // it, and on gfx950 that overwrite reached memory (component 1, the next instruction's
+    // target) for some lanes; with a constant soffset the wait states are inserted
+    if constexpr (sizeof(OutT) == 4) {
+      // row-plane rp = 4 * i + lane / 16 of instruction i, channels 4 * (lane % 16) .. + 3
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        const int rp = 4 * i + (lane >> 4), plane = rp / R, row = rp % R, piece = lane & 15;
+        const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
+        u32x4 q;
+        q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
+        q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
+        const int off = off0 + 16 * piece + row * row_bytes + plane * plane_bytes;
+        __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
+      }
+    } else {
+      // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
+#pragma unroll
+      for (int i = 0; i < R / 2; ++i) {
+        const int rp = 8 * i + (lane >> 3), plane = rp / R, row = rp % R, piece = lane & 7;
+        const float4 a = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece);
+        const float4 c = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece + 4);
+        u32x4 q;
+        q.x = bf16_pair(a.x, a.y); q.y = bf16_pair(a.z, a.w);
+        q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
+        const int off = off0 + 16 * piece + row * row_bytes + plane * plane_bytes;
+        __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
+      }
+    }
+  }
+
+  // materialize() through a per-wave LDS region `stage` (4 planes x R rows x 64 floats): each
+  // group of R rows is written to LDS one channel per lane and stored by store_stage. The tile's
+  // 64 channels must all lie below C.
   static constexpr int kStageRows = L >= 16 ? 4 : 2;  // R
-  template <typename OutT, bool NORM, int R = kStageRows>
+  template <typename OutT, int R = kStageRows>
   __device__ __forceinline__ void materialize_lds(rsrc_t w, int lane, int so0, int row_bytes,
                                                   int plane_bytes, int ch_bytes0, int n,
                                                   float* stage, const float* lr, const float* li,
-                                                  float* sr, float* si, float scale,
-                                                  const float (*nw)[K]) const {
+                                                  float* sr, float* si) const {
     static_assert(K == 1 && L % R == 0 && R % 2 == 0, "LDS-staged stores: one channel per lane, whole groups");
 #pragma unroll
     for (int g = 0; g < L / R; ++g) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         const int j = R * g + r;
-        const float mr = lr[0] * sr[0] - li[0] * si[0];
-        const float mi = lr[0] * si[0] + li[0] * sr[0];
-        float o[4];
-        o[2] = fmaf(-gk[j][0], mr, mr);
-        o[3] = fmaf(-gk[j][0], mi, mi);
+        float o[4] = {sr[0], si[0], 0.f, 0.f};
+        step(j, 0, lr[0], li[0], o[0], o[1], o[2], o[3]);
         if (j < n) {  // rows from n on lie past T: their stores are dropped, the state stops here
-          sr[0] = fmaf(gk[j][0], mr, gbr[j][0]);
-          si[0] = fmaf(gk[j][0], mi, gbi[j][0]);
-        }
-        o[0] = sr[0];
-        o[1] = si[0];
-        if constexpr (NORM) {
-          const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), j));
-#pragma unroll
-          for (int p = 0; p < 4; ++p) o[p] = (o[p] * sc) * nw[p][0];
+          sr[0] = o[0];
+          si[0] = o[1];
         }
 #pragma unroll
         for (int p = 0; p < 4; ++p) stage[(p * R + r) * 64 + lane] = o[p];
       }
-      // soffset stays the constant 0: a 16-byte store with an SGPR soffset is not covered by
-      // the compiler's wait states for a VALU op overwriting the store's data VGPRs right after
-      // it, and on gfx950 that overwrite reached memory (component 1, the next instruction's
-      // target) for some lanes; with a constant soffset the wait states are inserted
-      if constexpr (sizeof(OutT) == 4) {
-        // row-plane rp = 4 * i + lane / 16 of instruction i, channels 4 * (lane % 16) .. + 3
+      store_stage<OutT, R>(w, lane, so0 + R * g * row_bytes + ch_bytes0, row_bytes, plane_bytes, stage);
+    }
+  }
+
+  // RMSNorm epilogue (K = 1), value pass over rows j0 .. j0 + H - 1: the four read values
+  // (Re s, Im s, Re disp, Im disp) of each row from (sr, si), kept in v for the stores, and each
+  // row's sum of their squares in ss (0 for rows j >= n, which lie past T, and for lanes outside
+  // the channel range, ok false). The state stops at row n - 1; the values of rows past it are
+  // never stored.
+  template <int H>
+  __device__ __forceinline__ void norm_values(int j0, int n, bool ok, float lr, float li, float& sr,
+                                              float& si, float (&v)[L][4], float (&ss)[H]) const {
+    static_assert(K == 1, "the RMSNorm epilogue runs one channel per lane");
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-          const int rp = 4 * i + (lane >> 4), plane = rp / R, row = rp % R, piece = lane & 15;
-          const float4 v = *reinterpret_cast<const float4*>(stage + rp * 64 + 4 * piece);
-          u32x4 q;
-          q.x = __float_as_uint(v.x); q.y = __float_as_uint(v.y);
-          q.z = __float_as_uint(v.z); q.w = __float_as_uint(v.w);
-          const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
-          __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
-        }
-      } else {
-        // row-plane rp = 8 * i + lane / 8 of instruction i, channels 8 * (lane % 8) .. + 7
+    for (int i = 0; i < H; ++i) {
+      const int j = j0 + i;
+      v[j][0] = sr;
+      v[j][1] = si;
+      step(j, 0, lr, li, v[j][0], v[j][1], v[j][2], v[j][3]);
+      if (j < n) {
+        sr = v[j][0];
+        si = v[j][1];
+      }
+      float acc = v[j][0] * v[j][0];
+      acc = fmaf(v[j][1], v[j][1], acc);
+      acc = fmaf(v[j][2], v[j][2], acc);
+      acc = fmaf(v[j][3], v[j][3], acc);
+      ss[i] = (ok && j < n) ? acc : 0.f;
+    }
+  }
+
+  // RMSNorm epilogue, stores of rows j0 .. j0 + H - 1 through LDS: row j stores
+  // (v[j][p] * scale_j) * nw[p], scale_j taken from lane j - j0 of `scale`, in groups of R rows
+  // by store_stage (the tile's 64 channels must all lie below C).
+  template <typename OutT, int H, int R = kStageRows>
+  __device__ __forceinline__ static void store_norm_lds(rsrc_t w, int lane, int j0, int so0,
+                                                        int row_bytes, int plane_bytes,
+                                                        int ch_bytes0, float* stage,
+                                                        const float (&v)[L][4], float scale,
+                                                        const float (&nw)[4]) {
+    static_assert(H % R == 0 && R % 2 == 0, "LDS-staged stores: whole groups");
 #pragma unroll
-        for (int i = 0; i < R / 2; ++i) {
-          const int rp = 8 * i + (lane >> 3), plane = rp / R, row = rp % R, piece = lane & 7;
-          const float4 a = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece);
-          const float4 c = *reinterpret_cast<const float4*>(stage + rp * 64 + 8 * piece + 4);
-          u32x4 q;
-          q.x = bf16_pair(a.x, a.y); q.y = bf16_pair(a.z, a.w);
-          q.z = bf16_pair(c.x, c.y); q.w = bf16_pair(c.z, c.w);
-          const int off = so0 + R * g * row_bytes + ch_bytes0 + 16 * piece + row * row_bytes + plane * plane_bytes;
-          __builtin_amdgcn_raw_buffer_store_b128(q, w, off, 0, kStreamStore);
+    for (int g = 0; g < H / R; ++g) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const int i = R * g + r;
+        const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), i));
+#pragma unroll
+        for (int p = 0; p < 4; ++p) stage[(p * R + r) * 64 + lane] = (v[j0 + i][p] * sc) * nw[p];
+      }
+      store_stage<OutT, R>(w, lane, so0 + (j0 + R * g) * row_bytes + ch_bytes0, row_bytes,
+                           plane_bytes, stage);
+    }
+  }
+
+  // RMSNorm epilogue, register stores of rows j0 .. j0 + H - 1: row j < n stores
+  // (v[j][p] * scale_j) * nw[p] from lanes with ok set.
+  template <typename OutT, int H>
+  __device__ __forceinline__ static void store_norm(rsrc_t w, int vo, int j0, int so0, int row_bytes,
+                                                    int plane_bytes, int n, bool ok,
+                                                    const float (&v)[L][4], float scale,
+                                                    const float (&nw)[4]) {
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      const int j = j0 + i;
+      const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), i));
+      if (ok && j < n) {
+        const int so = so0 + j * row_bytes;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const float o = (v[j][p] * sc) * nw[p];
+          ReadStore<OutT, 1>::run(w, vo, so + p * plane_bytes, &o);
         }
       }
     }
@@ -450,84 +534,12 @@ struct WaveTile {
       if (j < n) {
         float dr[K], di[K];
 #pragma unroll
-        for (int k = 0; k < K; ++k) {
-          // m = lam*s_prev, disp = v*m = m - keep*m, s = keep*m + b
-          const float mr = lr[k] * sr[k] - li[k] * si[k];
-          const float mi = lr[k] * si[k] + li[k] * sr[k];
-          dr[k] = fmaf(-gk[j][k], mr, mr);
-          di[k] = fmaf(-gk[j][k], mi, mi);
-          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
-          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
-        }
+        for (int k = 0; k < K; ++k) step(j, k, lr[k], li[k], sr[k], si[k], dr[k], di[k]);
         const int so = so0 + j * row_bytes;
         ReadStore<OutT, K>::run(w, vo, so, sr);
         ReadStore<OutT, K>::run(w, vo, so + plane_bytes, si);
         ReadStore<OutT, K>::run(w, vo, so + 2 * plane_bytes, dr);
         ReadStore<OutT, K>::run(w, vo, so + 3 * plane_bytes, di);
-      }
-    }
-  }
-
-  // Per step j < n: sum over this lane's K channels of the squares of the four read values
-  // (Re s, Im s, Re disp, Im disp) of the recurrence from (sr0, si0); 0 for j >= n and for
-  // lanes outside the channel range (ok false).
-  __device__ __forceinline__ void sumsq(int n, bool ok, const float* lr, const float* li,
-                                        const float* sr0, const float* si0, float* ss) const {
-    float sr[K], si[K];
-#pragma unroll
-    for (int k = 0; k < K; ++k) { sr[k] = sr0[k]; si[k] = si0[k]; }
-#pragma unroll
-    for (int j = 0; j < L; ++j) {
-      float acc = 0.f;
-      if (j < n) {
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const float mr = lr[k] * sr[k] - li[k] * si[k];
-          const float mi = lr[k] * si[k] + li[k] * sr[k];
-          const float dr = fmaf(-gk[j][k], mr, mr), di = fmaf(-gk[j][k], mi, mi);
-          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
-          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
-          acc = fmaf(sr[k], sr[k], acc);
-          acc = fmaf(si[k], si[k], acc);
-          acc = fmaf(dr, dr, acc);
-          acc = fmaf(di, di, acc);
-        }
-      }
-      ss[j] = ok ? acc : 0.f;
-    }
-  }
-
-  // materialize() with the RMSNorm epilogue: row j stores (value * scale_j) * nw[plane][k],
-  // scale_j taken from lane j of `scale`. Every lane of the wave runs the recurrence (the
-  // scales are read across lanes); lanes with ok false store nothing.
-  template <typename OutT>
-  __device__ __forceinline__ void materialize_norm(rsrc_t w, int vo, int so0, int row_bytes,
-                                                   int plane_bytes, int n, bool ok,
-                                                   const float* lr, const float* li, float* sr,
-                                                   float* si, float scale,
-                                                   const float (*nw)[K]) const {
-#pragma unroll
-    for (int j = 0; j < L; ++j) {
-      if (j < n) {
-        const float sc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(scale), j));
-        float o[4][K];
-#pragma unroll
-        for (int k = 0; k < K; ++k) {
-          const float mr = lr[k] * sr[k] - li[k] * si[k];
-          const float mi = lr[k] * si[k] + li[k] * sr[k];
-          const float dr = fmaf(-gk[j][k], mr, mr), di = fmaf(-gk[j][k], mi, mi);
-          sr[k] = fmaf(gk[j][k], mr, gbr[j][k]);
-          si[k] = fmaf(gk[j][k], mi, gbi[j][k]);
-          o[0][k] = (sr[k] * sc) * nw[0][k];
-          o[1][k] = (si[k] * sc) * nw[1][k];
-          o[2][k] = (dr * sc) * nw[2][k];
-          o[3][k] = (di * sc) * nw[3][k];
-        }
-        if (ok) {
-          const int so = so0 + j * row_bytes;
-#pragma unroll
-          for (int p = 0; p < 4; ++p) ReadStore<OutT, K>::run(w, vo, so + p * plane_bytes, o[p]);
-        }
       }
     }
   }
@@ -880,7 +892,8 @@ __device__ __forceinline__ void rearm(LookbackHeader* hdr, uint32_t epoch) {
 }
 // One thread's count of its block toward the launch's end; the last block re-arms the counter.
 // Blocks that refused an out-of-range ticket count too, so a counter that was out of range is
-// re-armed by the launch that saw it.
+// re-armed by the launch that saw it. (The backward scan ends every block here: its reduction
+// launch, which runs after it, clears the workspace at the epoch wrap.)
 __device__ __forceinline__ void finish_block(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch) {
   const unsigned int d = atomicAdd(&hdr->done, 1u);
   if (d == n_tiles - 1) rearm(hdr, epoch);
@@ -897,33 +910,37 @@ struct ClearSpan {
 };
 constexpr uint32_t kEpochMask = 0x3fffffffu;  // bits of the epoch that published words carry
 
-// A forward tile block's end, called by every thread of the block: counts the block toward the
-// launch's end, and the launch's last block re-arms the counter for the next launch (next epoch).
-// Published words carry 30 bits of the epoch, so a word written 2^30 launches earlier would carry
-// the tag of the current one. In the launch whose next epoch's 30 bits wrap to 0 (the same epoch,
-// so the same branch, for every block), the last block therefore zero-fills the whole span first
-// (one thread: a few ms, once in 2^30 launches): every word any earlier launch left in the buffer
-// (at any shape's layout) goes, before any launch of the new cycle reads it. There every block
-// counts only after a barrier (all its waves are past their last access to published words) and
-// with release-acquire ordering, so the clear lands after every store of the launch and no wave
-// still reads what it clears. Every other launch counts with one thread and no barrier. (Code
-// here is in the kernel's tail; written this way it leaves the generated code of the kernel's
-// body as it is without it.) A block that refused an out-of-range ticket counts through
-// finish_block and never clears: such a launch has already set the error word.
+// A forward tile block's end, called by every thread of the block (blocks that refused an
+// out-of-range ticket included): counts the block toward the launch's end, and the launch's last
+// block re-arms the counter for the next launch (next epoch). Published words carry 30 bits of the
+// epoch, so a word written 2^30 launches earlier would carry the tag of the current one. In the
+// launch whose next epoch's 30 bits wrap to 0 (the same epoch, so the same branch, for every
+// block), the last block therefore zero-fills the whole span first, with the 64 lanes of its wave
+// 0 (16 bytes per lane and store): every word any earlier launch left in the buffer (at any
+// shape's layout) goes, before any launch of the new cycle reads it. There every block counts
+// only after a barrier (all its waves are past their last access to published words) and with
+// release-acquire ordering, so the clear lands after every store of the launch and no wave still
+// reads what it clears. Every other launch counts with one thread and no barrier. (Code here is in
+// the kernel's tail; written this way it leaves the generated code of the kernel's body as it is
+// without it.)
 __device__ __forceinline__ void finish_launch(LookbackHeader* hdr, uint32_t n_tiles, uint32_t epoch,
                                               const ClearSpan& clr) {
   const bool wrap = ((epoch + 1u) & kEpochMask) == 0u;
-  if (wrap) __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned int d =
-        wrap ? __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT)
-             : atomicAdd(&hdr->done, 1u);
+  if (!wrap) {
+    if (threadIdx.x == 0) finish_block(hdr, n_tiles, epoch);
+    return;
+  }
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    unsigned int d = 0u;
+    if (threadIdx.x == 0)
+      d = __hip_atomic_fetch_add(&hdr->done, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    d = __shfl(d, 0);
     if (d == n_tiles - 1) {
-      if (wrap) {
-        for (size_t i = 0; i < clr.na; ++i) clr.a[i] = make_uint4(0u, 0u, 0u, 0u);
-        for (size_t i = 0; i < clr.nb; ++i) clr.b[i] = make_uint4(0u, 0u, 0u, 0u);
-      }
-      rearm(hdr, epoch);
+      const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+      for (size_t i = threadIdx.x; i < clr.na; i += 64) clr.a[i] = z;
+      for (size_t i = threadIdx.x; i < clr.nb; i += 64) clr.b[i] = z;
+      if (threadIdx.x == 0) rearm(hdr, epoch);
     }
   }
 }
@@ -1097,6 +1114,52 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
   }
 }
 
+// RMSNorm scale of H rows of a wave: lane l returns rsqrt(total / 4C + eps) of row l mod H,
+// the total being the sum of the partial words of the n_ctiles channel tiles of the token
+// (sg + s * stride: tile s's word of lane l's row), added in the same order by every tile of the
+// token (lanes l, l + H, ... take every (64/H)-th tile in turn, then combine by xor shuffles).
+// Rows at or past n_valid take no words. A row whose total misses a partial (a wait that gave
+// up) gets a NaN scale and the header's error bit.
+template <int H>
+__device__ __forceinline__ float row_scale(const uint64_t* sg, size_t stride, int n_ctiles,
+                                           bool row_valid, uint32_t tag, uint32_t limit,
+                                           float inv_n, float eps, LookbackHeader* hdr, int lane) {
+  float tot = 0.f;
+  bool failed = false;
+  if (row_valid) {
+    uint32_t spins = 0;
+    constexpr int kStride = 64 / H, kBatch = 4;  // lanes per row; words in flight per lane
+    for (int s0 = lane / H; s0 < n_ctiles && !failed; s0 += kBatch * kStride) {
+      uint64_t w[kBatch];
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int sq = s0 + q * kStride;
+        w[q] = sq < n_ctiles ? get_word(const_cast<uint64_t*>(sg) + (size_t)sq * stride) : 0ull;
+      }
+#pragma unroll
+      for (int q = 0; q < kBatch; ++q) {
+        const int sq = s0 + q * kStride;
+        if (sq < n_ctiles && !failed) {
+          if (!settle_words<1>(const_cast<uint64_t*>(sg) + (size_t)sq * stride, 0, tag, &w[q],
+                               spins, limit)) {
+            failed = true;
+          } else {
+            tot += word_value(w[q]);
+          }
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = H; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
+  // the lanes holding a row's words (l, l + H, ...) combine their failures as their sums
+  int row_failed = failed ? 1 : 0;
+#pragma unroll
+  for (int m = H; m < 64; m <<= 1) row_failed |= __shfl_xor(row_failed, m);
+  if (__ballot(failed) != 0ull && lane == 0) report_error(hdr, 1u);
+  return row_failed ? poison() : rsqrtf(fmaf(tot, inv_n, eps));
+}
+
 // Block-order tile of block i with the channel tiles of a row group on one XCD. The dispatcher
 // sends block i to XCD i mod 8, so consecutive tickets (the channel tiles of one row group, the
 // same rows of raw and read) would land on eight XCDs. Within each window of 8 row groups
@@ -1171,10 +1234,9 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     // wave-uniform (SGPR) values: every descriptor and offset built from them stays scalar
     ticket = (uint32_t)uniform((int)s_tk[0]);
     if (ticket >= n_tiles) {  // counter out of range (not re-armed): refuse, terminate
-      if (threadIdx.x == 0) {
-        report_error(hdr, 2u);
-        finish_block(hdr, n_tiles, s_tk[1]);
-      }
+      if (threadIdx.x == 0) report_error(hdr, 2u);
+      // counts toward the launch's end like any block (and clears at the epoch wrap if last)
+      finish_launch(hdr, n_tiles, (uint32_t)uniform((int)s_tk[1]), wrap_clear);
       return;
     }
   }
@@ -1310,70 +1372,39 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       }
     }
     if constexpr (NORM) {
-      // partial sums of squares of this tile's rows, lane l holding row l mod L
-      float ss[L];
-      tile.sumsq(n_valid, ok, lr, li, sr, si, ss);
+      // The tile's read values are kept for the stores; the partial sums of squares of its rows
+      // (lane l holding row l mod L) are published for the sibling tiles of the token. (Rows
+      // exchanged in two or four parts, each published as soon as formed so that one part's
+      // exchange overlaps the next part's pass: cold B=8, T=2,048 35.8 -> 36.5 / 38.9 us.)
+      float v[L][4], ss[L];
+      tile.template norm_values<L>(0, n_valid, ok, lr[0], li[0], sr[0], si[0], v, ss);
       const float part = wave_row_sums<L>(ss, lane);
       const int row = lane & (L - 1);
       const uint32_t tag_sib = ((epoch & 0x3fffffffu) << 2) | kTagSib;
       if (lane < L && row < n_valid) put_word(sib + (size_t)ticket * TC + wave * L + row, part, tag_sib);
       // the norm weights are needed only after the exchange: load them now, under its wait
-      float nw[4][K];
+      float nw[4];
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int k = 0; k < K; ++k) nw[p][k] = ok ? norm_w[p * C + c0 + k] : 0.f;
-      // row totals over the group's channel tiles, summed in the same order by every tile
-      float tot = 0.f;
-      bool sib_failed = false;
-      if (row < n_valid) {
-        uint64_t* sg = sib + ((size_t)chunk * n_chains + (size_t)b * n_ctiles) * TC + wave * L + row;
-        uint32_t spins = 0;
-        constexpr int kStride = 64 / L, kBatch = 4;  // lanes per row; words in flight per lane
-        for (int s0 = lane / L; s0 < n_ctiles && !sib_failed; s0 += kBatch * kStride) {
-          uint64_t w[kBatch];
-#pragma unroll
-          for (int q = 0; q < kBatch; ++q) {
-            const int sq = s0 + q * kStride;
-            w[q] = sq < n_ctiles ? get_word(sg + (size_t)sq * TC) : 0ull;
-          }
-#pragma unroll
-          for (int q = 0; q < kBatch; ++q) {
-            const int sq = s0 + q * kStride;
-            if (sq < n_ctiles && !sib_failed) {
-              if (!settle_words<1>(sg + (size_t)sq * TC, 0, tag_sib, &w[q], spins, limit)) {
-                sib_failed = true;
-              } else {
-                tot += word_value(w[q]);
-              }
-            }
-          }
-        }
-      }
-#pragma unroll
-      for (int m = L; m < 64; m <<= 1) tot += __shfl_xor(tot, m);
-      // a row whose total misses a sibling's partial gets a NaN scale: the lanes holding the
-      // row's words (l, l + L, ...) combine their failures as they combine their sums
-      int row_failed = sib_failed ? 1 : 0;
-#pragma unroll
-      for (int m = L; m < 64; m <<= 1) row_failed |= __shfl_xor(row_failed, m);
-      if (__ballot(sib_failed) != 0ull && lane == 0) report_error(hdr, 1u);
-      const float scale = row_failed ? poison() : rsqrtf(fmaf(tot, inv_n, eps));
+      for (int p = 0; p < 4; ++p) nw[p] = ok ? norm_w[p * C + c0] : 0.f;
+      // sibling s's word of this lane's row
+      const uint64_t* const sg = sib + ((size_t)chunk * n_chains + (size_t)b * n_ctiles) * TC + wave * L + row;
+      const float scale = row_scale<L>(sg, TC, n_ctiles, row < n_valid, tag_sib, limit, inv_n, eps,
+                                       hdr, lane);
       if constexpr (LDSIO) {
         float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
-        tile.template materialize_lds<OutT, true>(io.read, lane, wave * L * io.read_row, io.read_row,
-                                                  io.read_plane, ctile * CT * (int)sizeof(OutT),
-                                                  n_valid, stage, lr, li, sr, si, scale, nw);
+        WaveTile<RawT, K, L>::template store_norm_lds<OutT, L>(
+            io.read, lane, 0, wave * L * io.read_row, io.read_row, io.read_plane,
+            ctile * CT * (int)sizeof(OutT), stage, v, scale, nw);
       } else {
-        tile.template materialize_norm<OutT>(io.read, io.vo_read, wave * L * io.read_row,
-                                             io.read_row, io.read_plane, n_valid, ok, lr, li, sr,
-                                             si, scale, nw);
+        WaveTile<RawT, K, L>::template store_norm<OutT, L>(io.read, io.vo_read, 0,
+                                                           wave * L * io.read_row, io.read_row,
+                                                           io.read_plane, n_valid, ok, v, scale, nw);
       }
     } else if constexpr (LDSIO) {
       float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
-      tile.template materialize_lds<OutT, false>(io.read, lane, wave * L * io.read_row, io.read_row,
-                                                 io.read_plane, ctile * CT * (int)sizeof(OutT),
-                                                 n_valid, stage, lr, li, sr, si, 0.f, nullptr);
+      tile.template materialize_lds<OutT>(io.read, lane, wave * L * io.read_row, io.read_row,
+                                          io.read_plane, ctile * CT * (int)sizeof(OutT), n_valid,
+                                          stage, lr, li, sr, si);
     } else {
       tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
                                      io.read_plane, n_valid, lr, li, sr, si);
@@ -1839,6 +1870,11 @@ __global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float*
   if (wave == 0) {
     float t = 0.f;
     for (int u = 0; u < NW; ++u) t += s_acc[u][lane];
+    // a tile whose block refused an out-of-range ticket (error bit 1, set by the scan launch)
+    // wrote no partials: its rows hold an earlier call's values, so the sums are poisoned
+    const uint32_t err = __hip_atomic_load(const_cast<unsigned int*>(&hdr->error), __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+    if (err & 2u) t = poison();
     const int c = ctile * CT + lane;
     if (c < C) (plane == 0 ? grad_tr : plane == 1 ? grad_ti : grad_gamma)[c] = t;
   }
@@ -1885,8 +1921,8 @@ __global__ __launch_bounds__(256) void fl_decode_step_kernel(
   for (int k = 0; k < K; ++k) {
     float keep, br, bi;
     gates(zr[k], zi[k], zv[k], kVacancyMax * gm[k], keep, br, bi);
-    const float mr = lr[k] * sr[k] - li[k] * si[k];
-    const float mi = lr[k] * si[k] + li[k] * sr[k];
+    float mr, mi;
+    cmul(lr[k], li[k], sr[k], si[k], mr, mi);
     dr[k] = fmaf(-keep, mr, mr);
     di[k] = fmaf(-keep, mi, mi);
     sr[k] = fmaf(keep, mr, br);
@@ -1913,8 +1949,8 @@ __device__ __forceinline__ void decode_one(float zr, float zi, float zv, float l
                                            float gm, float& sr, float& si, float& dr, float& di) {
   float keep, br, bi;
   gates(zr, zi, zv, kVacancyMax * gm, keep, br, bi);
-  const float mr = lr * sr - li * si;
-  const float mi = lr * si + li * sr;
+  float mr, mi;
+  cmul(lr, li, sr, si, mr, mi);
   dr = fmaf(-keep, mr, mr);
   di = fmaf(-keep, mi, mi);
   sr = fmaf(keep, mr, br);
@@ -2180,13 +2216,14 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? FL_OK : FL_ERR_HI
 
 // Look-back tilings: (K channels per lane, L steps per wave, W waves per block, OCC target
 // waves per SIMD, which caps the VGPR budget so that OCC*4/W blocks share a CU).
-// Variant 0 is the default; the others are selectable for tuning (algo >> 8).
+// Variant 0 is the default; the others are selectable for tuning (algo >> 8). Every one reaches
+// its occupancy target without scratch (a 32-step tiling at 4 waves per SIMD spilled, and the
+// default at 6 stayed at 4).
 struct LookbackTiling {
   int k, l, w, occ;
 };
 constexpr LookbackTiling kLookbackTilings[] = {
-    {1, 16, 8, 4}, {1, 16, 8, 2}, {1, 16, 8, 6}, {1, 32, 4, 4},
-    {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4},  {1, 16, 4, 4},
+    {1, 16, 8, 4}, {1, 16, 8, 2}, {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4}, {1, 16, 4, 4},
 };
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
 // The default tiling with LDS-staged raw loads and read stores (LDSIO) is what variant 0 runs for
@@ -2365,8 +2402,8 @@ int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T,
   } else {
     const LookbackTiling tl = kLookbackTilings[variant];
     const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
-    FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 16, 8, 6) FL_LB(1, 32, 4, 4) FL_LB(1, 32, 4, 3)
-    FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4) FL_LB(1, 16, 4, 4)
+    FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 32, 4, 3) FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4)
+    FL_LB(1, 16, 4, 4)
     // narrowed K (alignment): same L, W, OCC
     FL_LB(1, 16, 4, 3) FL_LB(1, 8, 8, 4)
   }

@@ -39,7 +39,7 @@ extern "C" {
 /* algorithm selector for fl_scan_forward_ex (low 8 bits); bits 8.. select a tiling variant of
  * FL_ALGO_LOOKBACK for tuning: 0 = default (LDS-staged 16-byte loads and stores where raw is bf16
  * with 16-byte aligned rows, read is fp32 and C is a multiple of 64; register loads and stores
- * otherwise), 1..7 = other tilings, 8 = LDS-staged where possible, 9 = default tiling with
+ * otherwise), 1..5 = other tilings, 6 = LDS-staged where possible, 7 = default tiling with
  * register loads and stores on every input */
 #define FL_ALGO_AUTO 0
 #define FL_ALGO_CHUNKED3 1 /* chunk summary -> chunk carry -> chunk materialise (three launches) */
@@ -76,6 +76,9 @@ extern "C" {
  *              workspace must be stream-ordered (one workspace per stream). Every launch advances
  *              an epoch kept there; the launch at each 2^30-launch wrap of its tag bits zero-fills
  *              the rest of the workspace itself, so it is never zero-filled again by the caller.
+ *   workspace_bytes  the size of that allocation. It must not exceed the allocation: the wrap
+ *              launch zero-fills workspace_bytes after the header (every word an earlier call at
+ *              any shape may have left), so a larger value writes past the buffer.
  *
  * Workspace header (first 2 KiB; little-endian words at these byte offsets):
  *   128  u32  error word: bit 0 a bounded wait gave up, bit 1 a ticket beyond the launch's tiles
@@ -164,7 +167,10 @@ int fl_scan_norm_forward(const void* raw, int raw_dtype, int64_t B, int64_t T, i
  *   grad_tr, grad_ti, grad_gamma  [C] fp32 (overwritten)
  *   grad_state_in   [B, 2C] fp32 planar, or NULL
  *   workspace       >= fl_scan_backward_workspace_bytes(B, T, C), 256-byte aligned, zero-filled
- *                   before first use, then reused (one per stream), as for fl_scan_forward
+ *                   before first use, then reused (one per stream), as for fl_scan_forward;
+ *                   workspace_bytes must not exceed the allocation (the same wrap clear)
+ * A block that finds the ticket counter out of range (error bit 1) computes nothing, so the
+ * parameter gradients of that call are NaN (its reduction sums every tile's partials).
  */
 int fl_scan_backward(const void* raw, int raw_dtype, int64_t B, int64_t T, int64_t C,
                      int64_t raw_stride_b, int64_t raw_stride_t, const float* tr, const float* ti,

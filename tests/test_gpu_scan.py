@@ -69,10 +69,10 @@ def test_scan_matches_oracle(dev, shape, dtype, algo):
     assert torch.isfinite(read).all()
 
 
-@pytest.mark.parametrize("variant", range(10))
+@pytest.mark.parametrize("variant", range(8))
 def test_lookback_tilings(dev, variant):
     """Every look-back tiling (algo bits 8..) on ragged shapes, fp32 and bf16, with state_in
-    (variants 0 and 8 stage the bf16 cases with full channel tiles through LDS, variant 9 never)."""
+    (variants 0 and 6 stage the bf16 cases with full channel tiles through LDS, variant 7 never)."""
     from fields_lm_amd import _native as nat
     from fields_lm_amd import field_scan
 
@@ -114,7 +114,7 @@ def test_lds_staged_io_equals_register_io(dev):
             a, sa = field_scan(*args, state_in=sin.to(dev), return_state=True, algo=nat.FL_ALGO_AUTO,
                                read_dtype=rd)
             b, sb = field_scan(*args, state_in=sin.to(dev), return_state=True,
-                               algo=nat.FL_ALGO_LOOKBACK | (9 << 8), read_dtype=rd)
+                               algo=nat.FL_ALGO_LOOKBACK | (7 << 8), read_dtype=rd)
             torch.cuda.synchronize()
             assert torch.equal(a, b) and torch.equal(sa, sb), (B, T, C, pad_t, pad_b, rd)
             if rd == torch.float32:
@@ -167,7 +167,7 @@ def test_workspace_reuse_across_shapes_and_algos(dev):
         raw = torch.randn(B, T, 3 * C, generator=g) * 2
         tr, ti, gamma = _params(C, seed=40 + i)
         cases.append((raw, tr, ti, gamma, oracle.scan_f64(raw, tr, ti, gamma)[0]))
-    algos = [nat.FL_ALGO_LOOKBACK, nat.FL_ALGO_CHUNKED3, nat.FL_ALGO_LOOKBACK | (3 << 8),
+    algos = [nat.FL_ALGO_LOOKBACK, nat.FL_ALGO_CHUNKED3, nat.FL_ALGO_LOOKBACK | (2 << 8),
              nat.FL_ALGO_LOOKBACK | (1 << 8), nat.FL_ALGO_AUTO]
     for rep in range(3):
         for ci, (raw, tr, ti, gamma, expect) in enumerate(cases):
@@ -305,13 +305,16 @@ def test_full_size_workloads(dev, name, algo):
 
     print(f"[case] full size {name} {algo}", flush=True)
     wl = make_scan_workload(name, dev)
-    code = nat.FL_ALGO_AUTO if algo == "auto" else nat.FL_ALGO_LOOKBACK | (9 << 8)
+    code = nat.FL_ALGO_AUTO if algo == "auto" else nat.FL_ALGO_LOOKBACK | (7 << 8)
     read, state = field_scan(wl.raw, wl.tr, wl.ti, wl.gamma, return_state=True, algo=code)
     torch.cuda.synchronize()
     exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
     got = read.cpu()
     assert oracle.rel_err(got, exp_read) <= TOL
     assert oracle.rel_err(state.cpu(), exp_state) <= TOL
+    # every token row's four planes (Re s, Im s, Re disp, Im disp) on their own scale
+    assert oracle.rel_err_rows(got, exp_read, planes=4) <= TOL
+    assert oracle.rel_err_rows(state.cpu(), exp_state, planes=2) <= TOL
     T = wl.raw.shape[1]
     C = wl.channels
     for t in range(2047, T, 2048):
@@ -497,6 +500,9 @@ def test_config1_block_rows_match_reference_golden(dev, golden_dir):
     y = y.cpu()
     assert oracle.rel_err(y[0, rows], d["block_rows"]) <= TOL
     assert oracle.rel_err(state[0].cpu(), d["final_state"].reshape(-1)) <= TOL
+    # each sampled row on its own scale, and the state's real and imaginary halves
+    assert oracle.rel_err_rows(y[0, rows], d["block_rows"]) <= TOL
+    assert oracle.rel_err_rows(state[0].cpu(), d["final_state"].reshape(-1), planes=2) <= TOL
 
 
 def test_block_prefill_then_steps_equal_forward(dev):

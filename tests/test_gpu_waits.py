@@ -124,6 +124,10 @@ def test_given_up_backward_wait_poisons_gradients(dev, monkeypatch):
     # tickets are taken in reverse time order: the tiles that ran hold the first rows in time
     # order 63..65 from the end, i.e. rows 0 .. 3*64; their carries were missing
     assert bool(torch.isnan(g_raw[:, :3 * 64]).all())
+    # the parameter gradients sum the partials of every tile, and the refused tiles wrote none:
+    # the reduction launch poisons them when the scan refused tickets
+    for grad in (g_tr, g_ti, g_gm):
+        assert bool(torch.isnan(grad).all())
     with pytest.raises(RuntimeError, match="wait give up"):
         field_scan_backward(raw, tr, ti, gamma, read, gread)
     nat.set_spin_limit(ws, 0)
@@ -240,3 +244,71 @@ def test_epoch_wrap_clears_published_words(dev, kind):
     for x, y in zip(after_large, ref_large):
         assert torch.equal(x, y)
     assert nat.workspace_error(ws) == 0
+
+
+def test_refused_launch_at_the_epoch_wrap_still_clears(dev, monkeypatch):
+    """A wrap launch whose every block refuses its ticket (the counter seeded past the launch's
+    tiles): the last block to count is one that refused, and it still zero-fills the workspace
+    after its header and re-arms the counter for the new cycle. Outputs are left untouched, the
+    next call raises, and the call after that is correct."""
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd import _native as nat
+
+    monkeypatch.setattr(nat, "CHECK_WAITS", False)  # the default reporting path, not the check mode
+    B, T, C = 1, 66 * 128, 64  # 66 chunks: tickets from the counter
+    print(f"[case] refused wrap launch B={B} T={T} C={C}", flush=True)
+    g = torch.Generator().manual_seed(31)
+    raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(torch.bfloat16).to(dev)
+    tr, ti, gamma = (t.to(dev) for t in _params(C, seed=7))
+    plan = ScanPlan(raw, tr, ti, gamma)
+    ws = plan.workspace
+    _plant_stale_words(ws)
+    _seed_counter(ws, epoch=(1 << 30) - 1, first_ticket=66)  # every ticket out of range
+    plan.read.fill_(7.0)
+    plan.run()
+    torch.cuda.synchronize()
+    assert nat.workspace_error(ws) & 2
+    assert bool((plan.read == 7.0).all())
+    assert int(ws[2048:].count_nonzero()) == 0
+    word = int(ws[TICKET_OFFSET:TICKET_OFFSET + 8].view(torch.int64).item())
+    assert word == (1 << 30) << 32  # re-armed: the new cycle's first epoch, ticket 0
+    with pytest.raises(RuntimeError, match="ticket"):
+        plan.run()
+    out = plan.run()
+    torch.cuda.synchronize()
+    assert nat.workspace_error(ws) == 0
+    exp, _ = oracle.scan_f64(raw.float().cpu(), tr.cpu(), ti.cpu(), gamma.cpu())
+    assert oracle.rel_err(out.cpu(), exp) <= 1e-4
+
+
+def test_epoch_wrap_clear_time_at_a_large_workspace(dev):
+    """The wrap launch's clear (one wave of the last block, 16 bytes per lane and store) on the
+    workspace of B=1, T=65,536, C=512 (config 4, ~67 MB): timed against an ordinary launch of the
+    same plan, and the workspace is zero after its header."""
+    from fields_lm_amd import ScanPlan
+    from fields_lm_amd.workloads import make_scan_workload
+
+    print("[case] epoch wrap clear time, config 4 workspace", flush=True)
+    wl = make_scan_workload("scan_b1_t65536_d1024", dev)
+    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma)
+    ws = plan.workspace
+    plan.run()
+    ref = plan.read.clone()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    plan.run()
+    b.record()
+    torch.cuda.synchronize()
+    ordinary_ms = a.elapsed_time(b)
+    _plant_stale_words(ws)
+    _seed_counter(ws, epoch=(1 << 30) - 1, first_ticket=0)
+    a.record()
+    plan.run()
+    b.record()
+    torch.cuda.synchronize()
+    wrap_ms = a.elapsed_time(b)
+    print(f"[case] workspace {ws.numel() / 1e6:.1f} MB: ordinary launch {ordinary_ms:.3f} ms, "
+          f"wrap launch {wrap_ms:.3f} ms", flush=True)
+    assert torch.equal(plan.read, ref)
+    assert int(ws[2048:].count_nonzero()) == 0
+    assert wrap_ms < 100.0
