@@ -170,3 +170,25 @@ def rel_err(actual, expected) -> float:
     denom = float(np.max(np.abs(e))) if e.size else 0.0
     diff = float(np.max(np.abs(a - e))) if e.size else 0.0
     return diff / max(denom, 1e-30)
+
+
+def rel_err_rows(actual, expected, planes: int = 1) -> float:
+    """Row-wise relative error: the last axis is split into ``planes`` equal planes (``read``'s
+    ``[Re s | Im s | Re disp | Im disp]``, ``grad_raw``'s three gate planes), every (row, plane)
+    is normalised by its own max|expected|, and the worst one is returned. An error confined to
+    small-magnitude rows or to one plane, which :func:`rel_err` divides by the tensor's largest
+    value, shows here. A (row, plane) whose expected values are all zero is compared absolutely."""
+    a = _f64(actual)
+    e = _f64(expected)
+    if a.shape != e.shape:
+        raise ValueError(f"shape mismatch {a.shape} vs {e.shape}")
+    if e.size == 0:
+        return 0.0
+    n = e.shape[-1]
+    if n % planes:
+        raise ValueError(f"last axis {n} does not split into {planes} planes")
+    a = a.reshape(-1, planes, n // planes)
+    e = e.reshape(-1, planes, n // planes)
+    diff = np.max(np.abs(a - e), axis=-1)
+    den = np.max(np.abs(e), axis=-1)
+    return float(np.max(diff / np.where(den > 0.0, den, 1.0)))

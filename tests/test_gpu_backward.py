@@ -154,6 +154,13 @@ def test_backward_full_size_config2_row(dev):
     e_raw, _, _, _, _ = _oracle_grads(wl.raw[row:row + 1].float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu(),
                                       gread[row:row + 1].cpu())
     assert oracle.rel_err(g_raw[row:row + 1].float().cpu(), e_raw) <= 4e-3
+    # row by row, each of grad_raw's three gate planes on its own scale: the bf16 output (2^-9
+    # relative rounding) and the fp32 output of the same values (raw upcast exactly)
+    assert oracle.rel_err_rows(g_raw[row:row + 1].float().cpu(), e_raw, planes=3) <= 4e-3
+    g32 = field_scan_backward(wl.raw[row:row + 1].float(), wl.tr, wl.ti, wl.gamma,
+                              read[row:row + 1].contiguous(), gread[row:row + 1].contiguous())[0]
+    assert oracle.rel_err(g32.cpu(), e_raw) <= TOL
+    assert oracle.rel_err_rows(g32.cpu(), e_raw, planes=3) <= TOL
     rows = [field_scan_backward(wl.raw[r:r + 1], wl.tr, wl.ti, wl.gamma, read[r:r + 1].contiguous(),
                                 gread[r:r + 1].contiguous())[1] for r in range(8)]
     assert oracle.rel_err(g_tr.cpu(), sum(x.double() for x in rows).cpu()) <= 1e-5

@@ -216,7 +216,8 @@ def test_norm_plan_graph_replays(dev):
 
 @pytest.mark.parametrize("name", ["scan_b8_t2048_d1024", "scan_b1_t65536_d1024"])
 def test_norm_full_size_workloads(dev, name):
-    """Configs 2 and 4: fused bf16 output against the float64 oracle's normalised read."""
+    """Configs 2 and 4: fused bf16 and fp32 outputs against the float64 oracle's normalised read,
+    norm-wise and token row by token row (each row's four planes on their own scale)."""
     from fields_lm_amd import ScanPlan
     from fields_lm_amd import _native as nat
     from fields_lm_amd.workloads import make_scan_workload
@@ -225,15 +226,20 @@ def test_norm_full_size_workloads(dev, name):
     wl = make_scan_workload(name, dev)
     C = wl.channels
     w = _weight(C, 4).to(dev)
-    plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, read_dtype=torch.bfloat16, norm_weight=w)
-    out = plan.run()
-    torch.cuda.synchronize()
-    assert nat.workspace_error(plan.workspace) == 0
     exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
     exp = oracle.rms_norm_f64(exp_read, w.cpu(), 1e-6)
     del exp_read
-    assert oracle.rel_err(out.float().cpu(), exp) <= 4e-3  # bf16 rounding: 2^-9 relative
-    assert oracle.rel_err(plan.state_out.cpu(), exp_state) <= TOL
+    for out_dtype, tol in ((torch.bfloat16, 4e-3), (torch.float32, TOL)):  # bf16: 2^-9 relative
+        plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, read_dtype=out_dtype, norm_weight=w)
+        out = plan.run()
+        torch.cuda.synchronize()
+        assert nat.workspace_error(plan.workspace) == 0
+        got = out.float().cpu()
+        assert oracle.rel_err(got, exp) <= tol, out_dtype
+        assert oracle.rel_err_rows(got, exp, planes=4) <= tol, out_dtype
+        assert oracle.rel_err(plan.state_out.cpu(), exp_state) <= TOL
+        assert oracle.rel_err_rows(plan.state_out.cpu(), exp_state, planes=2) <= TOL
+        del plan, out, got
 
 
 def test_norm_errors(dev):

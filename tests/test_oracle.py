@@ -314,3 +314,31 @@ def test_planted_sign_error_is_caught():
     swapped[..., :C], swapped[..., C:2 * C] = read[..., C:2 * C], read[..., :C]
     s2, _ = _split(swapped)
     assert not np.allclose(s2 + d, lam * prev + b, rtol=1e-6, atol=1e-9)
+
+
+def test_row_wise_metric_sees_what_the_norm_wise_one_divides_away():
+    """oracle.rel_err_rows normalises every (row, plane) by its own scale: a 1e-3 relative error
+    in a row 1e-3 the size of the largest (an early displaced-readout row, say) is 1e-6 of the
+    tensor's maximum, under the 1e-4 bar of rel_err, but 1e-3 row by row. A planted error in one
+    plane of one row is attributed to that plane; an all-zero row is compared absolutely."""
+    rng = np.random.default_rng(12)
+    exp = rng.normal(size=(3, 5, 4 * 8))
+    exp[1, 2] *= 1e-3
+    got = exp.copy()
+    got[1, 2] *= 1.0 + 1e-3
+    assert oracle.rel_err(got, exp) < 1e-5
+    assert oracle.rel_err_rows(got, exp, planes=4) == pytest.approx(1e-3, rel=1e-6)
+    assert oracle.rel_err_rows(exp, exp, planes=4) == 0.0
+    # one plane of one row off by 2e-3 of that plane's own maximum
+    got = exp.copy()
+    k = int(np.argmax(np.abs(exp[0, 0, 16:24])))
+    got[0, 0, 16 + k] += 2e-3 * np.abs(exp[0, 0, 16:24]).max()
+    assert oracle.rel_err_rows(got, exp, planes=4) == pytest.approx(2e-3, rel=1e-6)
+    assert oracle.rel_err_rows(got, exp, planes=1) < 2e-3
+    # an expected row of zeros: absolute difference
+    exp0 = np.zeros((2, 8))
+    got0 = exp0.copy()
+    got0[1, 3] = 5e-5
+    assert oracle.rel_err_rows(got0, exp0) == pytest.approx(5e-5)
+    with pytest.raises(ValueError):
+        oracle.rel_err_rows(np.zeros((2, 6)), np.zeros((2, 6)), planes=4)
