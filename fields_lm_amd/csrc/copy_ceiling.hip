@@ -13,6 +13,10 @@
 //   fl_bench_device_delay one wave that sleeps until the constant-rate wall clock has advanced by a
 //                         given number of ticks, queued before a timed loop's start event so that
 //                         the host has its first launches queued when the device reaches it
+//   fl_bench_occupy       `blocks` blocks of 1024 threads holding 112 KB of LDS each (so no scan
+//                         tile block fits beside one on its CU), each sleeping on the wall clock
+//                         for a given time: CUs held by another stream's bounded work, the
+//                         contention under which the tests run the scan's block-order launches
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -100,6 +104,28 @@ __global__ __launch_bounds__(64) void delay_kernel(uint64_t ticks) {
   while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
 }
 
+// One CU's worth of LDS held for `ticks` of the wall clock (bounded: every block exits).
+constexpr int kOccupyLdsFloats = 112 * 1024 / 4;
+__global__ __launch_bounds__(1024) void occupy_kernel(uint64_t ticks, float* sink) {
+  __shared__ float hold[kOccupyLdsFloats];
+  for (int i = threadIdx.x; i < kOccupyLdsFloats; i += 1024) hold[i] = (float)i;
+  __syncthreads();
+  const uint64_t t0 = wall_clock64();
+  while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+  // a value read back from the array, so that the compiler keeps it; never true
+  if (hold[(threadIdx.x * 37) % kOccupyLdsFloats] < -1.0f) sink[threadIdx.x] = hold[threadIdx.x];
+}
+
+int wall_ticks(double us, uint64_t* ticks) {
+  int dev = 0, khz = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
+  if (e != hipSuccess) return (int)e;
+  if (khz <= 0) return 1;
+  *ticks = (uint64_t)(us * (double)khz / 1000.0);
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -137,13 +163,21 @@ int fl_bench_stream_copy(const void* src, void* dst, size_t in_bytes, size_t out
 // Queues ~`us` microseconds of device time (one wave) on `stream`; at most 10 ms.
 int fl_bench_device_delay(double us, void* stream) {
   if (!(us >= 0.0) || us > 10000.0) return 1;
-  int dev = 0, khz = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e == hipSuccess) e = hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev);
-  if (e != hipSuccess) return (int)e;
-  if (khz <= 0) return 1;
-  const uint64_t ticks = (uint64_t)(us * (double)khz / 1000.0);
+  uint64_t ticks = 0;
+  const int rc = wall_ticks(us, &ticks);
+  if (rc != 0) return rc;
   delay_kernel<<<1, 64, 0, static_cast<hipStream_t>(stream)>>>(ticks);
+  return (int)hipGetLastError();
+}
+
+// Queues `blocks` (1..256) blocks that each hold one CU's LDS for ~`us` microseconds (at most
+// 10 ms) on `stream`. `sink` is a device buffer of 1024 floats that is never written in practice.
+int fl_bench_occupy(int blocks, double us, void* sink, void* stream) {
+  if (blocks < 1 || blocks > 256 || !(us >= 0.0) || us > 10000.0 || sink == nullptr) return 1;
+  uint64_t ticks = 0;
+  const int rc = wall_ticks(us, &ticks);
+  if (rc != 0) return rc;
+  occupy_kernel<<<blocks, 1024, 0, static_cast<hipStream_t>(stream)>>>(ticks, static_cast<float*>(sink));
   return (int)hipGetLastError();
 }
 
