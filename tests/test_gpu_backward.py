@@ -76,7 +76,7 @@ def test_backward_matches_oracle_gradients(dev, shape, dtype):
     torch.cuda.synchronize()
     e_raw, e_tr, e_ti, e_gm, e_sin = _oracle_grads(raw.float(), tr, ti, gamma, gread, sin, gso)
     assert g_raw.dtype == dtype
-    tol_raw = TOL if dtype == torch.float32 else 4e-3  # bf16 rounding of grad_raw: 2^-9 relative
+    tol_raw = TOL if dtype == torch.float32 else 4e-3  # bf16 rounding of grad_raw: at most 2^-8 relative
     assert oracle.rel_err(g_raw.float().cpu(), e_raw) <= tol_raw
     assert oracle.rel_err(g_tr.cpu(), e_tr) <= TOL
     assert oracle.rel_err(g_ti.cpu(), e_ti) <= TOL
@@ -154,13 +154,16 @@ def test_backward_full_size_config2_row(dev):
     e_raw, _, _, _, _ = _oracle_grads(wl.raw[row:row + 1].float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu(),
                                       gread[row:row + 1].cpu())
     assert oracle.rel_err(g_raw[row:row + 1].float().cpu(), e_raw) <= 4e-3
-    # row by row, each of grad_raw's three gate planes on its own scale: the bf16 output (2^-9
+    # row by row, each of grad_raw's three gate planes on its own scale: the bf16 output (2^-8
     # relative rounding) and the fp32 output of the same values (raw upcast exactly)
     assert oracle.rel_err_rows(g_raw[row:row + 1].float().cpu(), e_raw, planes=3) <= 4e-3
     g32 = field_scan_backward(wl.raw[row:row + 1].float(), wl.tr, wl.ti, wl.gamma,
                               read[row:row + 1].contiguous(), gread[row:row + 1].contiguous())[0]
+    e_rows = oracle.rel_err_rows(g32.cpu(), e_raw, planes=3)
+    print(f"[case] backward config 2 fp32 grad_raw: norm-wise {oracle.rel_err(g32.cpu(), e_raw):.2e}, "
+          f"row-wise {e_rows:.2e}", flush=True)
     assert oracle.rel_err(g32.cpu(), e_raw) <= TOL
-    assert oracle.rel_err_rows(g32.cpu(), e_raw, planes=3) <= TOL
+    assert e_rows <= TOL
     rows = [field_scan_backward(wl.raw[r:r + 1], wl.tr, wl.ti, wl.gamma, read[r:r + 1].contiguous(),
                                 gread[r:r + 1].contiguous())[1] for r in range(8)]
     assert oracle.rel_err(g_tr.cpu(), sum(x.double() for x in rows).cpu()) <= 1e-5

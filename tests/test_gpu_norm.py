@@ -229,14 +229,17 @@ def test_norm_full_size_workloads(dev, name):
     exp_read, exp_state = oracle.scan_f64(wl.raw.float().cpu(), wl.tr.cpu(), wl.ti.cpu(), wl.gamma.cpu())
     exp = oracle.rms_norm_f64(exp_read, w.cpu(), 1e-6)
     del exp_read
-    for out_dtype, tol in ((torch.bfloat16, 4e-3), (torch.float32, TOL)):  # bf16: 2^-9 relative
+    for out_dtype, tol in ((torch.bfloat16, 4e-3), (torch.float32, TOL)):  # bf16 rounds to within 2^-8 relative
         plan = ScanPlan(wl.raw, wl.tr, wl.ti, wl.gamma, read_dtype=out_dtype, norm_weight=w)
         out = plan.run()
         torch.cuda.synchronize()
         assert nat.workspace_error(plan.workspace) == 0
         got = out.float().cpu()
+        e_rows = oracle.rel_err_rows(got, exp, planes=4)
+        print(f"[case] scan_norm full size {name} {out_dtype}: norm-wise {oracle.rel_err(got, exp):.2e}, "
+              f"row-wise {e_rows:.2e}", flush=True)
         assert oracle.rel_err(got, exp) <= tol, out_dtype
-        assert oracle.rel_err_rows(got, exp, planes=4) <= tol, out_dtype
+        assert e_rows <= tol, out_dtype
         assert oracle.rel_err(plan.state_out.cpu(), exp_state) <= TOL
         assert oracle.rel_err_rows(plan.state_out.cpu(), exp_state, planes=2) <= TOL
         del plan, out, got

@@ -234,7 +234,7 @@ def test_bf16_read_is_rounded_fp32_read(dev, algo):
         torch.testing.assert_close(r16, r32.to(torch.bfloat16), rtol=0, atol=0)
         torch.testing.assert_close(s16, s32, rtol=0, atol=0)
         exp_read, _ = oracle.scan_f64(raw.float(), tr.cpu(), ti.cpu(), gamma.cpu(), state_in=sin)
-        assert oracle.rel_err(r16.float().cpu(), exp_read) <= 4e-3  # bf16 rounding: 2^-9 relative
+        assert oracle.rel_err(r16.float().cpu(), exp_read) <= 4e-3  # bf16 rounding: at most 2^-8 relative
 
 
 def test_scan_state_in_continuation(dev):
@@ -313,7 +313,10 @@ def test_full_size_workloads(dev, name, algo):
     assert oracle.rel_err(got, exp_read) <= TOL
     assert oracle.rel_err(state.cpu(), exp_state) <= TOL
     # every token row's four planes (Re s, Im s, Re disp, Im disp) on their own scale
-    assert oracle.rel_err_rows(got, exp_read, planes=4) <= TOL
+    e_rows = oracle.rel_err_rows(got, exp_read, planes=4)
+    print(f"[case] full size {name} {algo}: norm-wise {oracle.rel_err(got, exp_read):.2e}, "
+          f"row-wise {e_rows:.2e}", flush=True)
+    assert e_rows <= TOL
     assert oracle.rel_err_rows(state.cpu(), exp_state, planes=2) <= TOL
     T = wl.raw.shape[1]
     C = wl.channels
