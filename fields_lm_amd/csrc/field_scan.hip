@@ -27,6 +27,7 @@
 #include <stdint.h>
 #include <stddef.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "fields_amd.h"
@@ -956,6 +957,7 @@ __device__ __forceinline__ void finish_launch(LookbackHeader* hdr, uint32_t n_ti
 #define FL_DIRECT_CHUNKS 8
 #endif
 constexpr int kDirectChunks = FL_DIRECT_CHUNKS;
+
 constexpr int kLookbackBatch = 2;  // predecessor summaries in flight per wave
 // Look-back window: the predecessors whose summaries one round stages in LDS (3 x CT floats
 // each): 8W/K, at most 64 (one status load)
@@ -1002,13 +1004,16 @@ __device__ __forceinline__ bool settle_words(uint64_t* p, int stride, uint32_t t
 // and scans again (an inclusive state reaches every tile within kWin of the lowest unfinished
 // one, whose own predecessor is finished). On return wave 0 holds the carry-in in (cr, ci)
 // (NaN if a wait gave up after ``limit`` polls, with the error bit set). ``ord`` is the tile's
-// position in its chain's processing order; every predecessor is a full tile. Tiles at positions
-// up to kDirectChunks take n = ord - 1 (the inclusive state of position 0) without a scan and
-// wait on those words directly; the carry is the same bits (position 0's inclusive state with
-// every later summary applied), and the wait ends like any other (a predecessor's words are
-// published by a block that is resident or done, or the bounded wait gives up).
+// position in its chain's processing order; every predecessor is a full tile. Some tiles skip the
+// scan and wait on a predecessor set fixed in advance: with span > 0 (a block-order launch whose
+// resident blocks hold span positions of every chain per round) the summaries of their round's
+// earlier positions and the inclusive state of the previous round's last position; with span 0,
+// tiles at positions up to kDirectChunks, from the inclusive state of position 0. The carry is the
+// same bits either way (a predecessor's inclusive state with every later summary applied), and the
+// wait ends like any other (every predecessor has a lower ticket, so its words are published by a
+// block that is resident or done, or the bounded wait gives up).
 template <int K, int W, int kWin>
-__device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks, const uint32_t* st_chain,
+__device__ __forceinline__ void lookback_carry(int ord, int span, int chain, int n_chunks, const uint32_t* st_chain,
                                                uint64_t* data, uint32_t tag_agg, uint32_t tag_incl,
                                                const float* lTr, const float* lTi, bool ok, int lane,
                                                int wave, LookbackHeader* hdr, uint32_t limit,
@@ -1037,11 +1042,20 @@ __device__ __forceinline__ void lookback_carry(int ord, int chain, int n_chunks,
     if (lane == 0) { s_meta[0] = n; s_meta[1] = ready; }
   };
   if (wave == 0) {
-    if (ord <= kDirectChunks && ord <= kWin) {
-      // one of the first chunks of its chain: its predecessors are known without a status scan
-      // (the summaries of ord-1 .. 1 and the inclusive state of chunk 0), so every wave waits on
-      // those words directly, one round trip fewer
-      if (lane == 0) { s_meta[0] = j0; s_meta[1] = 1; }
+    // Direct wait: n summaries and the inclusive state of predecessor j0 - n, without a scan
+    int nd = -1;
+    if (span > 0) {
+      // `span` positions of each chain per round of resident blocks (block order): the tile waits
+      // on its own round's earlier summaries and the inclusive state of the previous round's last
+      // position (position 0's in the first round)
+      const int r0 = (ord / span) * span;
+      nd = r0 == 0 ? ord - 1 : ord - r0;
+      if (nd >= kWin) nd = -1;
+    } else if (ord <= kDirectChunks && ord <= kWin) {
+      nd = j0;  // one of the first chunks: the summaries of ord-1 .. 1, position 0's inclusive state
+    }
+    if (nd >= 0) {
+      if (lane == 0) { s_meta[0] = nd; s_meta[1] = 1; }
     } else {
       scan_status();
     }
@@ -1213,8 +1227,11 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, bool in_order,
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, int round_span,
     const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib, ClearSpan wrap_clear) {
+  // round_span > 0: block order (block i takes tile i), round_span chain positions per round of
+  // resident blocks; 0: tickets from the counter
+  const bool in_order = round_span > 0;
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1355,8 +1372,12 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     ci[k] = (ok && state_in) ? state_in[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
   }
   if (chunk > 0)
-    lookback_carry<K, W, kWin>(chunk, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi, ok,
-                               lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
+    // span 0: the first-positions rule only. Direct waits in later rounds too (the previous
+    // round's last inclusive state, which is often late here) measured slower for the forward:
+    // cold B=8, T=2,048 fp32 read 38.2-38.4 -> 38.9-39.1 us, RMSNorm epilogue 34.7-34.9 ->
+    // 35.1-36.0 us
+    lookback_carry<K, W, kWin>(chunk, 0, chain, n_chunks, st_chain, data, tag_agg, tag_incl, lTr, lTi,
+                               ok, lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -1482,7 +1503,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
     float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
     float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
-    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, bool in_order) {
+    float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, int round_span) {
+  const bool in_order = round_span > 0;  // as in the forward kernel
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -1684,8 +1706,10 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     ci[k] = (ok && grad_state_out) ? grad_state_out[(int64_t)b * 2 * C + C + c0 + k] : 0.f;
   }
   if (ord > 0)
-    lookback_carry<K, W, kWin>(ord, chain, n_chunks, st_chain, data, tag_agg, tag_incl, cTr, cTi, ok,
-                               lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
+    // direct waits in every round of a block-order launch: cold B=8, T=2,048 (four rounds of
+    // 64-step tiles) 59.8-60.3 -> 58.4-59.0 us against the first-positions rule alone
+    lookback_carry<K, W, kWin>(ord, round_span, chain, n_chunks, st_chain, data, tag_agg, tag_incl,
+                               cTr, cTi, ok, lane, wave, hdr, limit, s_pred, s_carry, s_meta, cr, ci);
   if (wave == 0) {
 #pragma unroll
     for (int k = 0; k < K; ++k) {
@@ -2378,6 +2402,26 @@ WsRegions regions_of(void* workspace, size_t workspace_bytes_given, int64_t B, i
           clear_span_after_header(workspace, workspace_bytes_given)};
 }
 
+constexpr int kMaxDevices = 64;  // devices the library keeps per-device state for
+
+// Chain positions per round of resident blocks in a block-order launch: blocks_per_cu x the
+// device's CU count (read once per device), divided among n_chains chains; at least 1. A hint for
+// the look-back's direct waits only: results and progress do not depend on it.
+int round_span(hipStream_t stream, int blocks_per_cu, int64_t n_chains) {
+  static std::atomic<int> cus[kMaxDevices];
+  int dev = 0;
+  if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
+  int n = dev >= 0 ? cus[dev].load(std::memory_order_relaxed) : 0;
+  if (n <= 0) {
+    if (dev < 0 || hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    if (dev >= 0) cus[dev].store(n, std::memory_order_relaxed);
+  }
+  const int64_t span = (int64_t)blocks_per_cu * n / (n_chains > 0 ? n_chains : 1);
+  return span < 1 ? 1 : (int)(span > (1 << 20) ? (1 << 20) : span);
+}
+
 template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
 int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb, int64_t st,
                     const float* tr, const float* ti, const float* gamma, const float* state_in,
@@ -2394,10 +2438,11 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // start, which the look-back needs to keep up (B=1, T=65,536: 155 us; 203 us in block order,
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
+  const int span = in_order ? round_span(stream, OCC * 4 / W, (int64_t)g.n_tiles / g.n_chunks) : 0;
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
-      g.n_tiles, in_order, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, rg.clr);
+      g.n_tiles, span, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, rg.clr);
   return hip_status(hipGetLastError());
 }
 
@@ -2516,6 +2561,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   const int64_t n_chains = B * (int64_t)g.n_ctiles;
   // ticket order as in the forward launch: block order for short chains, one counter otherwise
   const bool in_order = g.n_chunks <= 64;
+  const int span = in_order ? round_span(stream, tl.occ * 4 / tl.w, n_chains) : 0;
   // LDS-staged second-pass raw: every channel tile full, raw rows 16-byte aligned
   const int64_t esz = (int64_t)sizeof(RawT);
   const bool pf = FL_BWD_PREFETCH && C % CT == 0 && aligned(raw, 16) && (st * esz) % 16 == 0 &&
@@ -2526,7 +2572,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
       grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
-      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, in_order)
+      reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, span)
   if (pf) {
     FL_BWK(true);
   } else {
@@ -2664,7 +2710,6 @@ constexpr size_t kStaticDataOff = kStaticStatusOff + ((size_t)kStaticMaxTiles * 
 constexpr size_t kStaticScratchBytes = kStaticDataOff + (size_t)kStaticMaxTiles * kPlanes * 64 * 8;
 static_assert(kStaticScratchBytes == FL_STATIC_SCRATCH_BYTES, "scratch size stated in fields_amd.h");
 static_assert(kStaticScratchBytes % 16 == 0, "zero-filled in 16-byte stores");
-constexpr int kMaxDevices = 64;
 }  // namespace
 
 static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
