@@ -1224,11 +1224,13 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
     int n_ctiles, const float* __restrict__ tr, const float* __restrict__ ti,
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     float* __restrict__ state_out, OutT* __restrict__ read, LookbackHeader* hdr,
-    uint32_t* status, uint64_t* data, uint32_t n_tiles, int round_span,
+    uint32_t* status, uint64_t* data, uint32_t n_tiles, int round_span, uint32_t raise_from,
     const float* __restrict__ norm_w, float eps, float inv_n, uint64_t* sib, ClearSpan wrap_clear) {
   // round_span > 0: block order (block i takes tile i), round_span chain positions per round of
-  // resident blocks; 0: tickets from the counter
+  // resident blocks; 0: tickets from the counter. Blocks from raise_from on (the launch's last
+  // half-round) issue at raised wave priority.
   const bool in_order = round_span > 0;
+  if (blockIdx.x >= raise_from) __builtin_amdgcn_s_setprio(2);
   constexpr int CT = 64 * K;
   constexpr int TC = W * L;
   static_assert(OCC * 4 >= W, "occupancy target below one block per CU");
@@ -2405,10 +2407,8 @@ WsRegions regions_of(void* workspace, size_t workspace_bytes_given, int64_t B, i
 
 constexpr int kMaxDevices = 64;  // devices the library keeps per-device state for
 
-// Chain positions per round of resident blocks in a block-order launch: blocks_per_cu x the
-// device's CU count (read once per device), divided among n_chains chains; at least 1. A hint for
-// the look-back's direct waits only: results and progress do not depend on it.
-int round_span(hipStream_t stream, int blocks_per_cu, int64_t n_chains) {
+// CU count of the stream's device, read once per device (256 if the query fails).
+int device_cus(hipStream_t stream) {
   static std::atomic<int> cus[kMaxDevices];
   int dev = 0;
   if (hipStreamGetDevice(stream, &dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) dev = -1;
@@ -2419,8 +2419,27 @@ int round_span(hipStream_t stream, int blocks_per_cu, int64_t n_chains) {
       n = 256;
     if (dev >= 0) cus[dev].store(n, std::memory_order_relaxed);
   }
-  const int64_t span = (int64_t)blocks_per_cu * n / (n_chains > 0 ? n_chains : 1);
+  return n;
+}
+
+// Chain positions per round of resident blocks in a block-order launch: blocks_per_cu x the
+// device's CU count, divided among n_chains chains; at least 1. A hint for the look-back's direct
+// waits only: results and progress do not depend on it.
+int round_span(hipStream_t stream, int blocks_per_cu, int64_t n_chains) {
+  const int64_t span = (int64_t)blocks_per_cu * device_cus(stream) / (n_chains > 0 ? n_chains : 1);
   return span < 1 ? 1 : (int)(span > (1 << 20) ? (1 << 20) : span);
+}
+
+// First block of the forward launch's raised tail: the last half-round of resident blocks
+// (blocks_per_cu x CUs / 2) when at least a full round of blocks comes before it, else n_tiles
+// (none). Those blocks start while the previous round's blocks still hold the other slots of their
+// CUs, and on a SIMD the older waves issue first, so they would otherwise finish last and set the
+// kernel's end. In round 1 the same stagger is what lets round 2 start early, so round 1 is never
+// raised. Issue order only: results do not depend on it.
+uint32_t tail_raise_from(hipStream_t stream, int blocks_per_cu, uint32_t n_tiles) {
+  const int64_t resident = (int64_t)blocks_per_cu * device_cus(stream);
+  const int64_t from = (int64_t)n_tiles - resident / 2;
+  return from >= resident ? (uint32_t)from : n_tiles;
 }
 
 template <typename RawT, typename OutT, int K, int L, int W, int OCC, bool NORM, bool LDSIO = false>
@@ -2440,10 +2459,15 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
   const int span = in_order ? round_span(stream, OCC * 4 / W, (int64_t)g.n_tiles / g.n_chunks) : 0;
+  // raised tail: not for the RMSNorm epilogue's counter-ticket launches (B=1, T=65,536: 142.3 ->
+  // 144.0 us with it, where the plain scan gains 148.9 -> 147.6 us)
+  const uint32_t raise_from =
+      (in_order || !NORM) ? tail_raise_from(stream, OCC * 4 / W, g.n_tiles) : g.n_tiles;
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
-      g.n_tiles, span, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)), rg.sib, rg.clr);
+      g.n_tiles, span, raise_from, norm.weight, norm.eps, (float)(1.0 / (4.0 * (double)C)),
+      rg.sib, rg.clr);
   return hip_status(hipGetLastError());
 }
 
