@@ -1903,6 +1903,12 @@ __global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float*
   const int lane = threadIdx.x & 63;
   const int wave = uniform(threadIdx.x >> 6);
   const int ctile = (int)blockIdx.x / 3, plane = (int)blockIdx.x - 3 * ctile;
+  // the header words first, so that their round trip overlaps the partials' (the scan launch
+  // that set them has ended)
+  const uint32_t err = __hip_atomic_load(const_cast<unsigned int*>(&hdr->error), __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t next_epoch = (uint32_t)(__hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED,
+                                                           __HIP_MEMORY_SCOPE_AGENT) >> 32);
   const float* base = part + ((size_t)ctile * 3 + plane) * n_rows * CT + lane;
   const int rpw = (n_rows + NW - 1) / NW;
   const int r0 = min(wave * rpw, n_rows), r1 = min(r0 + rpw, n_rows);
@@ -1922,14 +1928,10 @@ __global__ __launch_bounds__(1024) void fl_param_grad_reduce_kernel(const float*
     for (int u = 0; u < NW; ++u) t += s_acc[u][lane];
     // a tile whose block refused an out-of-range ticket (error bit 1, set by the scan launch)
     // wrote no partials: its rows hold an earlier call's values, so the sums are poisoned
-    const uint32_t err = __hip_atomic_load(const_cast<unsigned int*>(&hdr->error), __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
     if (err & 2u) t = poison();
     const int c = ctile * CT + lane;
     if (c < C) (plane == 0 ? grad_tr : plane == 1 ? grad_ti : grad_gamma)[c] = t;
   }
-  const uint32_t next_epoch = (uint32_t)(__hip_atomic_load(&hdr->ticket, __ATOMIC_RELAXED,
-                                                           __HIP_MEMORY_SCOPE_AGENT) >> 32);
   if ((next_epoch & kEpochMask) == 0u) {  // uniform over the grid
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     const uint4 z = make_uint4(0u, 0u, 0u, 0u);
