@@ -49,6 +49,8 @@ constexpr uint32_t kBufDword3 = 0x00020000u;  // gfx9 raw-buffer descriptor word
 typedef unsigned short bf16_bits;
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -115,8 +117,12 @@ struct RawLoad<bf16_bits, 4, POL> {
 __device__ __forceinline__ uint32_t bf16_bits_of(float x) {
   return (uint32_t)__builtin_bit_cast(unsigned short, (__bf16)x);
 }
+// Two values rounded to nearest even and packed (lo in bits 15..0): one v_cvt_pk_bf16_f32 with
+// both operands, where two scalar conversions compile to two of them, a shift and an OR
+// (cold B=8, T=2,048: bf16 read, RMSNorm epilogue). Bit-identical to bf16_bits_of on each half.
 __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
-  return bf16_bits_of(lo) | (bf16_bits_of(hi) << 16);
+  const f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2));
 }
 
 // Output stores (read, grad_raw) are streamed: written once, never read back by the kernel. The
@@ -1449,9 +1455,14 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       }
     } else if constexpr (LDSIO) {
       float* stage = reinterpret_cast<float*>(s_io) + wave * kStage;
-      tile.template materialize_lds<OutT>(io.read, lane, wave * L * io.read_row, io.read_row,
-                                          io.read_plane, ctile * CT * (int)sizeof(OutT), n_valid,
-                                          stage, lr, li, sr, si);
+      if (n_valid == L)  // every row in range: the row checks fold away
+        tile.template materialize_lds<OutT>(io.read, lane, wave * L * io.read_row, io.read_row,
+                                            io.read_plane, ctile * CT * (int)sizeof(OutT), L,
+                                            stage, lr, li, sr, si);
+      else
+        tile.template materialize_lds<OutT>(io.read, lane, wave * L * io.read_row, io.read_row,
+                                            io.read_plane, ctile * CT * (int)sizeof(OutT), n_valid,
+                                            stage, lr, li, sr, si);
     } else {
       tile.template materialize<OutT>(io.read, io.vo_read, wave * L * io.read_row, io.read_row,
                                      io.read_plane, n_valid, lr, li, sr, si);
@@ -2461,10 +2472,10 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
   const int span = in_order ? round_span(stream, OCC * 4 / W, (int64_t)g.n_tiles / g.n_chunks) : 0;
-  // raised tail: not for the RMSNorm epilogue's counter-ticket launches (B=1, T=65,536: 142.3 ->
-  // 144.0 us with it, where the plain scan gains 148.9 -> 147.6 us)
-  const uint32_t raise_from =
-      (in_order || !NORM) ? tail_raise_from(stream, OCC * 4 / W, g.n_tiles) : g.n_tiles;
+  // raised tail: plain scans only. The RMSNorm epilogue gains nothing from it in block order
+  // (B=8, T=2,048: 34.21 -> 34.20 us) and loses with counter tickets (B=1, T=65,536: 142.3 ->
+  // 144.0 us, where the plain scan gains 148.9 -> 147.6 us).
+  const uint32_t raise_from = NORM ? g.n_tiles : tail_raise_from(stream, OCC * 4 / W, g.n_tiles);
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
       gamma, state_in, state_out, static_cast<OutT*>(read), rg.hdr, rg.status, rg.data,
