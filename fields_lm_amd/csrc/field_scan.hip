@@ -440,9 +440,10 @@ struct WaveTile {
 
   // RMSNorm epilogue (K = 1), value pass over rows j0 .. j0 + H - 1: the four read values
   // (Re s, Im s, Re disp, Im disp) of each row from (sr, si), kept in v for the stores, and each
-  // row's sum of their squares in ss (0 for rows j >= n, which lie past T, and for lanes outside
-  // the channel range, ok false). The state stops at row n - 1; the values of rows past it are
-  // never stored.
+  // row's sum of their squares in ss (0 for lanes outside the channel range, ok false). Rows from
+  // n on lie past T: the pass runs through them with no row check (from zero input; their values
+  // and sums are never stored or published), and on return (sr, si) is the state after row n - 1,
+  // read back from v where the tile is partial (n is wave-uniform, j0 < n <= j0 + H).
   template <int H>
   __device__ __forceinline__ void norm_values(int j0, int n, bool ok, float lr, float li, float& sr,
                                               float& si, float (&v)[L][4], float (&ss)[H]) const {
@@ -453,15 +454,22 @@ struct WaveTile {
       v[j][0] = sr;
       v[j][1] = si;
       step(j, 0, lr, li, v[j][0], v[j][1], v[j][2], v[j][3]);
-      if (j < n) {
-        sr = v[j][0];
-        si = v[j][1];
-      }
+      sr = v[j][0];
+      si = v[j][1];
       float acc = v[j][0] * v[j][0];
       acc = fmaf(v[j][1], v[j][1], acc);
       acc = fmaf(v[j][2], v[j][2], acc);
       acc = fmaf(v[j][3], v[j][3], acc);
-      ss[i] = (ok && j < n) ? acc : 0.f;
+      ss[i] = ok ? acc : 0.f;
+    }
+    if (n < j0 + H) {
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        if (j0 + i == n - 1) {
+          sr = v[j0 + i][0];
+          si = v[j0 + i][1];
+        }
+      }
     }
   }
 
@@ -1426,7 +1434,8 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_lookback_kernel(
       // exchanged in two or four parts, each published as soon as formed so that one part's
       // exchange overlaps the next part's pass: cold B=8, T=2,048 35.8 -> 36.5 / 38.9 us.)
       float v[L][4], ss[L];
-      tile.template norm_values<L>(0, n_valid, ok, lr[0], li[0], sr[0], si[0], v, ss);
+      // (LDSIO: every channel of the tile lies below C, so every lane is in range)
+      tile.template norm_values<L>(0, n_valid, LDSIO || ok, lr[0], li[0], sr[0], si[0], v, ss);
       const int row = lane & (L - 1);
       const uint32_t tag_sib = ((epoch & 0x3fffffffu) << 2) | kTagSib;
       static_assert(L == 16 && kWin * 3 * CT >= W * 1024, "row sums staged in the look-back region");
