@@ -2289,13 +2289,13 @@ inline int hip_status(hipError_t e) { return e == hipSuccess ? FL_OK : FL_ERR_HI
 // Look-back tilings: (K channels per lane, L steps per wave, W waves per block, OCC target
 // waves per SIMD, which caps the VGPR budget so that OCC*4/W blocks share a CU).
 // Variant 0 is the default; the others are selectable for tuning (algo >> 8). Every one reaches
-// its occupancy target without scratch (a 32-step tiling at 4 waves per SIMD spilled, and the
-// default at 6 stayed at 4).
+// its occupancy target without scratch (a 32-step tiling at 4 waves per SIMD spilled, the
+// default at 6 stayed at 4, and two channels per lane with 16-step waves spilled 2 VGPRs at 3).
 struct LookbackTiling {
   int k, l, w, occ;
 };
 constexpr LookbackTiling kLookbackTilings[] = {
-    {1, 16, 8, 4}, {1, 16, 8, 2}, {1, 32, 4, 3}, {2, 16, 4, 3}, {2, 8, 8, 4}, {1, 16, 4, 4},
+    {1, 16, 8, 4}, {1, 16, 8, 2}, {1, 32, 4, 3}, {2, 16, 4, 2}, {2, 8, 8, 4}, {1, 16, 4, 4},
 };
 constexpr int kNumLookbackTilings = sizeof(kLookbackTilings) / sizeof(kLookbackTilings[0]);
 // The default tiling with LDS-staged raw loads and read stores (LDSIO) is what variant 0 runs for
@@ -2517,10 +2517,10 @@ int dispatch_lookback(int variant, int k, const void* raw, int64_t B, int64_t T,
   } else {
     const LookbackTiling tl = kLookbackTilings[variant];
     const int kk = tl.k <= k ? tl.k : k;  // never wider than the alignment allows
-    FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 32, 4, 3) FL_LB(2, 16, 4, 3) FL_LB(2, 8, 8, 4)
+    FL_LB(1, 16, 8, 4) FL_LB(1, 16, 8, 2) FL_LB(1, 32, 4, 3) FL_LB(2, 16, 4, 2) FL_LB(2, 8, 8, 4)
     FL_LB(1, 16, 4, 4)
     // narrowed K (alignment): same L, W, OCC
-    FL_LB(1, 16, 4, 3) FL_LB(1, 8, 8, 4)
+    FL_LB(1, 16, 4, 2) FL_LB(1, 8, 8, 4)
   }
 #undef FL_LB
   return FL_ERR_INVALID_ARGUMENT;
