@@ -2456,8 +2456,9 @@ int round_span(hipStream_t stream, int blocks_per_cu, int64_t n_chains) {
 // (blocks_per_cu x CUs / 2) when at least a full round of blocks comes before it, else n_tiles
 // (none). Those blocks start while the previous round's blocks still hold the other slots of their
 // CUs, and on a SIMD the older waves issue first, so they would otherwise finish last and set the
-// kernel's end. In round 1 the same stagger is what lets round 2 start early, so round 1 is never
-// raised. Issue order only: results do not depend on it.
+// kernel's end. In the launch's first round of resident blocks the same stagger is what lets the
+// second round start early, so the first round is never raised. Issue order only: results do not
+// depend on it.
 uint32_t tail_raise_from(hipStream_t stream, int blocks_per_cu, uint32_t n_tiles) {
   const int64_t resident = (int64_t)blocks_per_cu * device_cus(stream);
   const int64_t from = (int64_t)n_tiles - resident / 2;
