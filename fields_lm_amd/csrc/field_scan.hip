@@ -2482,9 +2482,9 @@ int launch_lookback(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   // 216 us with eight counters).
   const bool in_order = g.n_chunks <= 64;
   const int span = in_order ? round_span(stream, OCC * 4 / W, (int64_t)g.n_tiles / g.n_chunks) : 0;
-  // raised tail: plain scans only. The RMSNorm epilogue gains nothing from it in block order
-  // (B=8, T=2,048: 34.21 -> 34.20 us) and loses with counter tickets (B=1, T=65,536: 142.3 ->
-  // 144.0 us, where the plain scan gains 148.9 -> 147.6 us).
+  // raised tail: plain scans only. The RMSNorm epilogue loses with counter tickets (B=1,
+  // T=65,536: 142.3 -> 144.0 us, where the plain scan gains 148.9 -> 147.6 us) and gains at most
+  // 0.5 us in block order (B=8, T=2,048); it keeps plain priority.
   const uint32_t raise_from = NORM ? g.n_tiles : tail_raise_from(stream, OCC * 4 / W, g.n_tiles);
   fl_scan_lookback_kernel<RawT, OutT, K, L, W, OCC, NORM, LDSIO><<<g.n_tiles, W * 64, 0, stream>>>(
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti,
