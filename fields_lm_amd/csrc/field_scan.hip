@@ -1655,25 +1655,19 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     float P[K], Qr[K], Qi[K];
 #pragma unroll
     for (int k = 0; k < K; ++k) { P[k] = 1.f; Qr[k] = 0.f; Qi[k] = 0.f; }
-    auto map_rows = [&](int n) {
 #pragma unroll
-      for (int j = L - 1; j >= 0; --j) {
-        if (j < n) {
+    for (int j = L - 1; j >= 0; --j) {
+      if (j < n_valid) {
 #pragma unroll
-          for (int k = 0; k < K; ++k) {
-            const float keep = 1.f - gv[j][k];
-            const float xr = fmaf(keep, Qr[k] + uR[j][k], gv[j][k] * dR[j][k]);
-            const float xi = fmaf(keep, Qi[k] + uI[j][k], gv[j][k] * dI[j][k]);
-            cmul(clr[k], cli[k], xr, xi, Qr[k], Qi[k]);
-            P[k] *= keep;
-          }
+        for (int k = 0; k < K; ++k) {
+          const float keep = 1.f - gv[j][k];
+          const float xr = fmaf(keep, Qr[k] + uR[j][k], gv[j][k] * dR[j][k]);
+          const float xi = fmaf(keep, Qi[k] + uI[j][k], gv[j][k] * dI[j][k]);
+          cmul(clr[k], cli[k], xr, xi, Qr[k], Qi[k]);
+          P[k] *= keep;
         }
       }
-    };
-    if (n_valid == L)  // every row in range: the row checks fold away
-      map_rows(L);
-    else
-      map_rows(n_valid);
+    }
 #pragma unroll
     for (int k = 0; k < K; ++k) {
       s_sum[wave][0][lane * K + k] = P[k];
