@@ -1813,9 +1813,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
         zi[j][k] = fmaf(-2.0f, __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(zi[j][k] * (2.0f * kLog2e))), 1.0f);
         pr[j][k] = sr;
         pi[j][k] = si;
-        // s_j, needed as p by row j + 1 (rows from n_valid on lie past T: their p is never used,
-        // so the update needs no row check)
-        if (j + 1 < L) {
+        if (j + 1 < n_valid) {  // s_j, needed as p by row j + 1
           const float v = gv[j][k], gvv = gm[k] * v;
           float mr, mi;
           cmul(lr[k], li[k], sr, si, mr, mi);
