@@ -109,7 +109,9 @@ def test_config3_prefill_full_size(dev, promoted):
         mixer.read_dtype = "auto"
     assert logits.shape == (4, 2048, 16384)
     assert bool(torch.isfinite(logits).all())
-    assert oracle.rel_err(last.float().cpu(), logits[:, -1].float().cpu()) <= TOL_BF16_MODEL
+    e_last = oracle.rel_err(last.float().cpu(), logits[:, -1].float().cpu())
+    print(f"[case] prefill last logits against the forward's: {e_last:.2e}", flush=True)
+    assert e_last <= TOL_BF16_MODEL
     assert len(hook.records) == 1
     raw, normed = hook.records[0]
     assert raw.shape == (4, 2048, 1536) and normed.dtype == torch.float32
@@ -191,7 +193,15 @@ def test_config5_decode_full_size(dev, promoted):
     got = torch.stack(eager, 1).float().cpu()
     assert bool(torch.isfinite(got).all())
     # the step consuming token P + i predicts token P + i + 1: the forward's logits at P + i
-    assert oracle.rel_err(got, logits[:, P:P + N].float().cpu()) <= TOL_BF16_MODEL
+    exp = logits[:, P:P + N].float().cpu()
+    e_all = oracle.rel_err(got, exp)
+    e_step = [oracle.rel_err(got[:, i], exp[:, i]) for i in range(N)]
+    e_row = torch.tensor([oracle.rel_err(got[r], exp[r]) for r in range(B)])
+    print(f"[case] config 5 decode logits: norm-wise {e_all:.2e}; per step "
+          f"{' '.join(f'{e:.1e}' for e in e_step)}; worst rows {e_row.topk(4).indices.tolist()} at "
+          f"{' '.join(f'{e:.1e}' for e in e_row.topk(4).values.tolist())}, median row "
+          f"{float(e_row.median()):.1e}", flush=True)
+    assert e_all <= TOL_BF16_MODEL
     # the hooked Field block's fused step against the float64 oracle step + RMSNorm
     params = fresh["params"][bi]
     tr, ti, gamma, w = (t.detach().float().cpu() for t in params)

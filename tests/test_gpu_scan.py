@@ -150,8 +150,12 @@ def test_lookback_results_do_not_depend_on_timing(dev, dtype):
             if first is None:
                 first = [x.clone() for x in got]
             else:
-                for a, b in zip(got, first):
-                    assert torch.equal(a, b), (B, T, C, rep)
+                for i, (a, b) in enumerate(zip(got, first)):
+                    if not torch.equal(a, b):
+                        bad = (a != b).flatten().nonzero().flatten()
+                        raise AssertionError(
+                            f"B={B} T={T} C={C} rep={rep}: output {i} {tuple(a.shape)} differs at "
+                            f"{bad.numel()} elements, first {bad[:16].tolist()}, last {bad[-4:].tolist()}")
 
 
 def test_workspace_reuse_across_shapes_and_algos(dev):
