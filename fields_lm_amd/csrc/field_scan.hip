@@ -1524,8 +1524,7 @@ __global__ __launch_bounds__(W * 64, OCC) void fl_scan_backward_kernel(
     const float* __restrict__ gamma, const float* __restrict__ state_in,
     const float* __restrict__ read, const float* __restrict__ grad_read,
     const float* __restrict__ grad_state_out, GradT* __restrict__ grad_raw,
-    float* __restrict__ grad_state_in, float* __restrict__ grad_tr, float* __restrict__ grad_ti,
-    float* __restrict__ grad_gamma, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
+    float* __restrict__ grad_state_in, LookbackHeader* hdr, uint32_t* status, uint64_t* data,
     float* __restrict__ part, uint32_t n_tiles, uint32_t n_chains, int round_span) {
   const bool in_order = round_span > 0;  // as in the forward kernel
   constexpr int CT = 64 * K;
@@ -2618,7 +2617,7 @@ int launch_backward(const void* raw, int64_t B, int64_t T, int64_t C, int64_t sb
   fl_scan_backward_kernel<RawT, GradT, tl.k, tl.l, tl.w, tl.occ, PF><<<g.n_tiles, tl.w * 64, 0, stream>>>( \
       static_cast<const RawT*>(raw), sb, st, (int)T, (int)C, g.n_chunks, g.n_ctiles, tr, ti, gamma, \
       state_in, read, grad_read, grad_state_out, static_cast<GradT*>(grad_raw), grad_state_in,     \
-      grad_tr, grad_ti, grad_gamma, reinterpret_cast<LookbackHeader*>(ws),                        \
+      reinterpret_cast<LookbackHeader*>(ws),                                                      \
       reinterpret_cast<uint32_t*>(ws + lay.status_off), reinterpret_cast<uint64_t*>(ws + lay.data_off), \
       reinterpret_cast<float*>(ws + lay.part_off), g.n_tiles, (uint32_t)n_chains, span)
   if (pf) {
