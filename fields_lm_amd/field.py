@@ -558,9 +558,6 @@ class IndependentVacancyField(nn.Module):
             self._packed = (key, w, b)
         return self._packed[1], self._packed[2]
 
-    def _readout(self, x: torch.Tensor, read: torch.Tensor) -> torch.Tensor:
-        return self._project(x, self.read_norm(read))
-
     def _project(self, x: torch.Tensor, normed: torch.Tensor) -> torch.Tensor:
         out = self.out_proj(normed)
         gate = torch.sigmoid(self.gate_proj(x))

@@ -139,11 +139,6 @@ def block_forward(p: Mapping[str, torch.Tensor], x: torch.Tensor, field_chunk: i
     return (y, read) if return_read else y
 
 
-def default_ff_hidden(dim: int) -> int:
-    """PackedSwiGLU default hidden size (canon:318-321)."""
-    return ((int(8 * dim / 3) + 63) // 64) * 64
-
-
 def init_radius_theta(channels: int) -> Tuple[torch.Tensor, torch.Tensor]:
     """Deterministic mixer init (canon:1156-1160)."""
     ring = torch.linspace(0.85, 0.999, channels)
