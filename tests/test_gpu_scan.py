@@ -132,7 +132,8 @@ def test_lookback_results_do_not_depend_on_timing(dev, dtype):
     window of 64 tiles."""
     from fields_lm_amd import field_scan, field_scan_backward, field_scan_norm
 
-    for (B, T, C) in [(16, 1000, 512), (2, 9000, 64), (1, 40000, 128), (8, 2048, 512)]:
+    for (B, T, C) in [(16, 1000, 512), (2, 9000, 64), (1, 40000, 128), (8, 2048, 512),
+                      (64, 2048, 512)]:  # the last: the promoted model's config-5 prompt
         print(f"[case] determinism B={B} T={T} C={C} {dtype}", flush=True)
         g = torch.Generator().manual_seed(B + T + C)
         raw = (torch.randn(B, T, 3 * C, generator=g) * 2).to(dtype).to(dev)
